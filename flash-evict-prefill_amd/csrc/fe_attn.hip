@@ -1,0 +1,719 @@
+// Fused prefill for gfx950: online-softmax attention (traversal 1) followed by an exact
+// replay of the QK^T tiles with each query row's final softmax statistics (traversal 2),
+// whose weighted column sums become per-KV-token importance.
+//
+// Semantics follow flash_evict/prefill.py:14-83 (kernel) and :102-137 (launch):
+//   * GQA map kvhead = head // (Hq/Hkv)                                    (prefill.py:26)
+//   * logits scaled by scale*log2(e), causal row >= key, exp2 online softmax (:45-54)
+//   * P rounded to the input dtype before P@V, FP32 accumulation            (:57)
+//   * out = acc / l in the input dtype                                      (:59-60)
+//   * replay only where (query block end) > N - W                           (:61)
+//   * w_q = exp(decay*(q-(N-1))) for N-W <= q < N, else 0                   (:66-67)
+//   * p = exp2(s - m_q) / l_q, column sums over queries and grouped heads   (:68-77)
+//   * x ||v_k||_1 when value weighted                                       (:78-81)
+//   * FP32 atomic accumulation into I[b, kvhead, k]                         (:82-83)
+//
+// The design is gfx950-native rather than a transcription of the Triton schedule:
+//   * one workgroup = 4 waves = 4*TPW row tiles; a row tile is 32 query positions of one
+//     query head, and all row tiles of a workgroup share one KV head, so every K/V tile
+//     staged in LDS serves all grouped query heads (GQA packing);
+//   * traversal 1 computes S^T = K Q^T on v_mfma_f32_32x32x16_{bf16,f16}: lanes hold
+//     query columns, registers hold keys, so the row max/sum are in-lane plus one
+//     v_permlane32_swap; O^T = V^T P^T takes P^T straight from the S^T accumulators;
+//   * V is transposed while it is staged into LDS (v_perm_b32 packing), with the key order
+//     inside each 16-key group permuted to match the accumulator layout of S^T, so the
+//     A operand of P@V is one 16-byte LDS read per lane;
+//   * traversal 2 swaps the MFMA operands (S = Q K^T) so that lanes hold keys: the column
+//     sum over queries is in-lane plus one lane swap; 1/l_q and w_q are folded into one
+//     exponent bias per row, so each replayed element costs one FMA, one v_exp_f32, one add;
+//   * the four waves' column sums meet in LDS and each workgroup issues one FP32 atomic
+//     per key; the value L1 norm multiplies the finished sums in a separate pass;
+//   * workgroups are issued heaviest-causal-first, with consecutive block ids on
+//     different KV heads (the hardware deals blocks round-robin over the 8 XCDs, so each
+//     XCD's L2 sees a small set of KV heads).
+#include <math.h>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "fe_common.h"
+#include "fe_internal.h"
+#include "../../include/flash_evict.h"
+
+namespace fe {
+
+typedef unsigned short u16;
+
+struct AttnArgs {
+  const u16* q;
+  const u16* k;
+  const u16* v;
+  u16* out;
+  float* imp;
+  long long qs[4], ks[4], vs[4];   // element strides {b, h, n, d}
+  int N, D, G, Hq, Hkv, BH;
+  int tiles_bh;                     // row tiles per (b, kv head): G * ceil(N/32)
+  int wg_bh;                        // workgroups per (b, kv head)
+  float scale_log2;                 // softmax scale * log2(e)
+  float abs_scale_log2;
+  float decay_log2;                 // recency_decay * log2(e)
+  int neg_scale;
+  int causal, score, win_lo;        // win_lo = N - W
+  int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
+};
+
+// Load 8 consecutive channels [d0, d0+8) of one row; zero beyond D.
+__device__ __forceinline__ u32x4 load8(const u16* row, long long sd, int d0, int D, int vec) {
+  if (vec) {
+    if (d0 < D) return *(const u32x4*)(row + d0);
+    return (u32x4){0u, 0u, 0u, 0u};
+  }
+  u32 w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int da = d0 + 2 * i, db = da + 1;
+    const u32 lo = da < D ? (u32)row[(long long)da * sd] : 0u;
+    const u32 hi = db < D ? (u32)row[(long long)db * sd] : 0u;
+    w[i] = lo | (hi << 16);
+  }
+  return (u32x4){w[0], w[1], w[2], w[3]};
+}
+
+template <int DP>
+struct Tile {
+  static constexpr int BN = 64;                 // keys per LDS tile (two 32-key sub-tiles)
+  static constexpr int NDC = DP / 16;           // 16-channel MFMA k-chunks of QK^T
+  static constexpr int NDT = DP / 32;           // 32-channel row tiles of O^T
+  static constexpr int KST = DP + 8;            // LDS row stride of K (elements)
+  static constexpr int VST = BN + 8;            // LDS row stride of V^T (elements)
+  static constexpr int KCH = DP / 8;            // 16-byte chunks per K/V row
+  static constexpr int KITEMS = BN * KCH;
+  static constexpr int KPT = (KITEMS + 255) / 256;
+  static constexpr int VITEMS = (BN / 4) * KCH; // (4-key group, chunk) items
+  static constexpr int VPT = (VITEMS + 255) / 256;
+  static constexpr size_t LDS_K = (size_t)2 * BN * KST * 2;
+  static constexpr size_t LDS_V = (size_t)2 * DP * VST * 2;
+  static constexpr size_t LDS_RED = (size_t)2 * 4 * BN * 4;
+  static constexpr size_t LDS = LDS_K + LDS_V + LDS_RED;
+};
+
+template <typename E, int DP, int TPW>
+__global__ __launch_bounds__(256) void fused_attn_score_kernel(const AttnArgs a) {
+  typedef Tile<DP> T;
+  constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, KST = T::KST, VST = T::VST;
+  constexpr int KCH = T::KCH, KITEMS = T::KITEMS, KPT = T::KPT, VITEMS = T::VITEMS, VPT = T::VPT;
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  constexpr float POS_INF = __builtin_huge_valf();
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  u16* kl = (u16*)smem;                                  // [2][BN][KST]
+  u16* vl = (u16*)(smem + T::LDS_K);                     // [2][DP][VST]
+  float* red = (float*)(smem + T::LDS_K + T::LDS_V);     // [2][4][BN]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hh = lane >> 5;
+  const int N = a.N, D = a.D;
+
+  // ---- work decode: heaviest query blocks first, consecutive ids on different KV heads
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
+  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
+  const int t_begin = wg * 4 * TPW;
+  const int t_end = min(a.tiles_bh, t_begin + 4 * TPW);
+  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);  // exclusive query bound
+  const int kv_end = a.causal ? wg_q_hi : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  int q0[TPW];
+  bool tv[TPW];
+  int head[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = t_begin + wv * TPW + j;
+    tv[j] = t < t_end;
+    const int tt = tv[j] ? t : t_begin;
+    q0[j] = (tt / a.G) * 32;
+    head[j] = hkv * a.G + (tt - (tt / a.G) * a.G);
+  }
+
+  // ---- Q fragments: lane (row l32, half hh) holds channels [16c + 8hh, +8)
+  u32x4 qf[TPW][NDC];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int qr = q0[j] + l32;
+    const bool ok = tv[j] && qr < N;
+    const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+#pragma unroll
+    for (int c = 0; c < NDC; ++c)
+      qf[j][c] = ok ? load8(qp, a.qs[3], 16 * c + 8 * hh, D, a.qvec) : (u32x4){0u, 0u, 0u, 0u};
+  }
+
+  const u16* kbase = a.k + b * a.ks[0] + hkv * a.ks[1];
+  const u16* vbase = a.v + b * a.vs[0] + hkv * a.vs[1];
+
+  auto kload = [&](int kb, u32x4 (&kr)[KPT]) {
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+      const int i = tid + 256 * r;
+      if (KITEMS % 256 == 0 || i < KITEMS) {
+        const int key = i / KCH, ch = i - key * KCH;
+        const int gk = kb + key;
+        kr[r] = gk < N ? load8(kbase + (long long)gk * a.ks[2], a.ks[3], ch * 8, D, a.kvec)
+                       : (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto kstore = [&](int buf, const u32x4 (&kr)[KPT]) {
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+      const int i = tid + 256 * r;
+      if (KITEMS % 256 == 0 || i < KITEMS) {
+        const int key = i / KCH, ch = i - key * KCH;
+        *(u32x4*)(kl + buf * BN * KST + key * KST + ch * 8) = kr[r];
+      }
+    }
+  };
+  // V item (kg, ch): keys 4kg..4kg+3 of the tile, channels 8ch..8ch+7. kg varies fastest so
+  // that one wave's transposed 8-byte writes cover all LDS banks.
+  auto vload = [&](int kb, u32x4 (&vr)[VPT][4]) {
+#pragma unroll
+    for (int r = 0; r < VPT; ++r) {
+      const int i = tid + 256 * r;
+      if (VITEMS % 256 == 0 || i < VITEMS) {
+        const int kg = i & 15, ch = i >> 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int gk = kb + 4 * kg + e;
+          vr[r][e] = gk < N ? load8(vbase + (long long)gk * a.vs[2], a.vs[3], ch * 8, D, a.vvec)
+                            : (u32x4){0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+  auto vstore = [&](int buf, const u32x4 (&vr)[VPT][4]) {
+#pragma unroll
+    for (int r = 0; r < VPT; ++r) {
+      const int i = tid + 256 * r;
+      if (VITEMS % 256 == 0 || i < VITEMS) {
+        const int kg = i & 15, ch = i >> 4;
+        // 4-key group g of a 16-key chunk lands at position 4*{0,2,1,3}[g]: the P^T
+        // accumulator row order of a 32x32 MFMA (row = 8*(i/4) + 4*half + i%4).
+        const int gi = kg & 3;
+        const int pos = 16 * (kg >> 2) + 4 * (((gi & 1) << 1) | (gi >> 1));
+        u16* dst = vl + buf * DP * VST + (ch * 8) * VST + pos;
+#pragma unroll
+        for (int dd = 0; dd < 8; ++dd) {
+          const u32 sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+          const int w = dd >> 1;
+          const u32 lo = __builtin_amdgcn_perm(vr[r][1][w], vr[r][0][w], sel);
+          const u32 hi = __builtin_amdgcn_perm(vr[r][3][w], vr[r][2][w], sel);
+          *(u32x2*)(dst + dd * VST) = (u32x2){lo, hi};
+        }
+      }
+    }
+  };
+
+  // ---- traversal 1: online-softmax attention
+  f32x16 o[TPW][NDT];
+  float m_run[TPW], l_run[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    m_run[j] = NEG_INF;
+    l_run[j] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = (f32x16){};
+  }
+
+  {
+    u32x4 kr[KPT];
+    u32x4 vr[VPT][4];
+    kload(0, kr);
+    vload(0, vr);
+    kstore(0, kr);
+    vstore(0, vr);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1;
+    const int kb = it * BN;
+    const bool more = it + 1 < ntiles;
+    u32x4 kr[KPT];
+    u32x4 vr[VPT][4];
+    if (more) {
+      kload(kb + BN, kr);
+      vload(kb + BN, vr);
+    }
+    const u16* kc = kl + cur * BN * KST;
+    const u16* vc = vl + cur * DP * VST;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kbs = kb + 32 * s;
+      if (kbs >= kv_end) break;
+      bool act[TPW];
+      bool any = false;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        act[j] = tv[j] && (!a.causal || kbs <= q0[j] + 31);
+        any |= act[j];
+      }
+      if (!any) continue;
+
+      f32x16 sacc[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) {
+        const u32x4 kf = *(const u32x4*)(kc + (32 * s + l32) * KST + 16 * c + 8 * hh);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+          if (act[j]) sacc[j] = E::mfma(kf, qf[j][c], sacc[j]);
+      }
+
+      u32x4 pb[TPW][2];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        if (!act[j]) continue;
+        const int qi = q0[j] + l32;
+        const bool need_mask = (a.causal && kbs + 31 > q0[j]) || kbs + 32 > N;
+        float p[16];
+        float mn, corr;
+        if (need_mask) {
+          bool ok[16];
+          float mr = NEG_INF;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kbs + 8 * (i >> 2) + 4 * hh + (i & 3);
+            ok[i] = key < N && (!a.causal || key <= qi);
+            const float sv = a.neg_scale ? -sacc[j][i] : sacc[j][i];
+            mr = fmaxf(mr, ok[i] ? sv : NEG_INF);
+          }
+          mr = half_swap_max(mr);
+          const float mt = (mr == NEG_INF) ? NEG_INF : mr * a.abs_scale_log2;
+          mn = fmaxf(m_run[j], mt);
+          corr = (mn == m_run[j]) ? 1.f : fast_exp2(m_run[j] - mn);
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            p[i] = ok[i] ? fast_exp2(fmaf(sacc[j][i], a.scale_log2, -mn)) : 0.f;
+        } else {
+          float mr = NEG_INF;
+          if (a.neg_scale) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mr = fmaxf(mr, -sacc[j][i]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mr = fmaxf(mr, sacc[j][i]);
+          }
+          mr = half_swap_max(mr);
+          const float mt = mr * a.abs_scale_log2;
+          mn = fmaxf(m_run[j], mt);
+          corr = (mn == m_run[j]) ? 1.f : fast_exp2(m_run[j] - mn);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) p[i] = fast_exp2(fmaf(sacc[j][i], a.scale_log2, -mn));
+        }
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ps += p[i];
+        l_run[j] = l_run[j] * corr + ps;
+        m_run[j] = mn;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[j][dt] *= corr;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+          pb[j][c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
+                              E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
+      }
+
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const u32x4 vf = *(const u32x4*)(vc + (32 * dt + l32) * VST + 32 * s + 16 * c2 + 8 * hh);
+#pragma unroll
+          for (int j = 0; j < TPW; ++j)
+            if (act[j]) o[j][dt] = E::mfma(vf, pb[j][c2], o[j][dt]);
+        }
+      }
+    }
+    if (more) {
+      kstore(cur ^ 1, kr);
+      vstore(cur ^ 1, vr);
+    }
+    __syncthreads();
+  }
+
+  // ---- finish rows: O = acc / l, stored in the input dtype
+  float l_tot[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    l_tot[j] = half_swap_sum(l_run[j]);
+    const int qi = q0[j] + l32;
+    if (!tv[j] || qi >= N) continue;
+    const float inv = 1.f / l_tot[j];
+    u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+        const float x0 = o[j][dt][4 * g4 + 0] * inv, x1 = o[j][dt][4 * g4 + 1] * inv;
+        const float x2 = o[j][dt][4 * g4 + 2] * inv, x3 = o[j][dt][4 * g4 + 3] * inv;
+        const u32 w0 = E::pack2(x0, x1), w1 = E::pack2(x2, x3);
+        if (a.ovec && d0 + 3 < D) {
+          *(u32x2*)(op + d0) = (u32x2){w0, w1};
+        } else {
+          if (d0 + 0 < D) op[d0 + 0] = (u16)(w0 & 0xffffu);
+          if (d0 + 1 < D) op[d0 + 1] = (u16)(w0 >> 16);
+          if (d0 + 2 < D) op[d0 + 2] = (u16)(w1 & 0xffffu);
+          if (d0 + 3 < D) op[d0 + 3] = (u16)(w1 >> 16);
+        }
+      }
+    }
+  }
+
+  // ---- traversal 2: replay with final statistics, weighted column sums -> importance
+  if (!a.score || wg_q_hi - 1 < a.win_lo) return;
+
+  // Row bias b_q = m_q + log2(l_q) - log2(w_q): p_q,k * w_q = exp2(s*scale - b_q).
+  // Rows outside the observation window (or past N) get +inf, i.e. weight 0.
+  float bias[TPW][16];
+  bool rin[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int qi = q0[j] + l32;
+    const bool live = tv[j] && qi < N && qi >= a.win_lo;
+    const float br = live ? (m_run[j] + fast_log2(l_tot[j]) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bias[j][i] = __shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+    rin[j] = tv[j] && q0[j] + 31 >= a.win_lo;
+  }
+
+  __syncthreads();  // all waves are done with the traversal-1 LDS buffers
+  {
+    u32x4 kr[KPT];
+    kload(0, kr);
+    kstore(0, kr);
+  }
+  __syncthreads();
+
+  float* imp_row = a.imp + (long long)bh * N;
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1;
+    const int kb = it * BN;
+    const bool more = it + 1 < ntiles;
+    u32x4 kr[KPT];
+    if (more) kload(kb + BN, kr);
+    const u16* kc = kl + cur * BN * KST;
+    float cs[2] = {0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kbs = kb + 32 * s;
+      if (kbs >= kv_end) break;
+      bool act[TPW];
+      bool any = false;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        act[j] = rin[j] && (!a.causal || kbs <= q0[j] + 31);
+        any |= act[j];
+      }
+      if (!any) continue;
+      f32x16 sacc[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) {
+        const u32x4 kf = *(const u32x4*)(kc + (32 * s + l32) * KST + 16 * c + 8 * hh);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+          if (act[j]) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
+      }
+      const int key = kbs + l32;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        if (!act[j]) continue;
+        const bool need_mask = a.causal && kbs + 31 > q0[j];
+        if (need_mask) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int qr = q0[j] + 8 * (i >> 2) + 4 * hh + (i & 3);
+            const float x = fast_exp2(fmaf(sacc[j][i], a.scale_log2, -bias[j][i]));
+            cs[s] += key > qr ? 0.f : x;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) cs[s] += fast_exp2(fmaf(sacc[j][i], a.scale_log2, -bias[j][i]));
+        }
+      }
+    }
+    cs[0] = half_swap_sum(cs[0]);
+    cs[1] = half_swap_sum(cs[1]);
+    float* rb = red + cur * 4 * BN + wv * BN;
+    if (hh == 0) {
+      rb[l32] = cs[0];
+      rb[32 + l32] = cs[1];
+    }
+    if (more) kstore(cur ^ 1, kr);
+    __syncthreads();
+    if (tid < BN) {
+      const float* rr = red + cur * 4 * BN;
+      const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
+      const int key = kb + tid;
+      if (key < N && sum != 0.f) unsafeAtomicAdd(imp_row + key, sum);
+    }
+  }
+}
+
+// importance[b, j, n] *= sum_d |v[b, j, n, d]|; eight lanes per token row.
+template <typename E>
+__global__ __launch_bounds__(256) void value_l1_scale_kernel(const u16* v, long long vs0, long long vs1,
+                                                             long long vs2, long long vs3, int Hkv, int N,
+                                                             int D, int vec, float* imp, long long rows) {
+  const long long row = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  float s = 0.f;
+  if (row < rows) {
+    const long long bh = row / N;
+    const int n = (int)(row - bh * N);
+    const long long b = bh / Hkv, h = bh - b * Hkv;
+    const u16* p = v + b * vs0 + h * vs1 + (long long)n * vs2;
+    for (int d0 = 8 * sub; d0 < D; d0 += 64) {
+      const u32x4 w = load8(p, vs3, d0, D, vec);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s += fabsf(E::to_f32((u16)(w[e] & 0xffffu)));
+        s += fabsf(E::to_f32((u16)(w[e] >> 16)));
+      }
+    }
+  }
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  if (row < rows && sub == 0) imp[row] *= s;
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* p, long long n) {
+  const long long stride = (long long)gridDim.x * 256;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+}
+
+hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, (long long)n);
+  return hipGetLastError();
+}
+
+namespace {
+
+typedef void (*FusedFn)(AttnArgs);
+
+struct FusedEntry {
+  FusedFn fn;
+  size_t lds;
+  const char* name;
+  bool attr_set;
+};
+
+template <typename E, int DP, int TPW>
+FusedEntry make_entry(const char* name) {
+  return FusedEntry{fused_attn_score_kernel<E, DP, TPW>, Tile<DP>::LDS, name, false};
+}
+
+// Padded channel counts: D is rounded up to the next entry.
+constexpr int kDP[] = {32, 64, 96, 128, 160, 192, 224, 256};
+constexpr int kNumDP = sizeof(kDP) / sizeof(kDP[0]);
+
+std::vector<FusedEntry>& fused_table() {
+  static std::vector<FusedEntry> t = {
+      make_entry<F16, 32, 1>("fused_attn_score<f16,32,1>"),   make_entry<F16, 64, 1>("fused_attn_score<f16,64,1>"),
+      make_entry<F16, 96, 1>("fused_attn_score<f16,96,1>"),   make_entry<F16, 128, 1>("fused_attn_score<f16,128,1>"),
+      make_entry<F16, 160, 1>("fused_attn_score<f16,160,1>"), make_entry<F16, 192, 1>("fused_attn_score<f16,192,1>"),
+      make_entry<F16, 224, 1>("fused_attn_score<f16,224,1>"), make_entry<F16, 256, 1>("fused_attn_score<f16,256,1>"),
+      make_entry<BF16, 32, 1>("fused_attn_score<bf16,32,1>"),   make_entry<BF16, 64, 1>("fused_attn_score<bf16,64,1>"),
+      make_entry<BF16, 96, 1>("fused_attn_score<bf16,96,1>"),   make_entry<BF16, 128, 1>("fused_attn_score<bf16,128,1>"),
+      make_entry<BF16, 160, 1>("fused_attn_score<bf16,160,1>"), make_entry<BF16, 192, 1>("fused_attn_score<bf16,192,1>"),
+      make_entry<BF16, 224, 1>("fused_attn_score<bf16,224,1>"), make_entry<BF16, 256, 1>("fused_attn_score<bf16,256,1>"),
+  };
+  return t;
+}
+
+std::mutex g_attr_mutex;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int vec_ok(const void* p, const int64_t* st, int64_t D) {
+  return st[3] == 1 && D % 8 == 0 && aligned16(p) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0;
+}
+
+}  // namespace
+
+void append_attn_resources(std::string& out) {
+  for (auto& e : fused_table()) {
+    hipFuncAttributes attr;
+    if (hipFuncGetAttributes(&attr, (const void*)e.fn) != hipSuccess) continue;
+    char buf[512];
+    snprintf(buf, sizeof(buf),
+             "{\"kernel\":\"%s\",\"registers_per_thread\":%d,\"lds_static_bytes\":%zu,"
+             "\"lds_dynamic_bytes\":%zu,\"scratch_bytes_per_thread\":%zu,\"max_threads_per_block\":%d},",
+             e.name, attr.numRegs, (size_t)attr.sharedSizeBytes, e.lds, (size_t)attr.localSizeBytes,
+             attr.maxThreadsPerBlock);
+    out += buf;
+  }
+}
+
+}  // namespace fe
+
+using namespace fe;
+
+extern "C" int fe_zero_f32(float* p, int64_t n, void* hip_stream) {
+  clear_error();
+  if (n < 0 || (n > 0 && p == nullptr)) {
+    set_error("fe_zero_f32: invalid pointer or size");
+    return FE_ERR_INVALID;
+  }
+  hipError_t err = launch_zero_f32(p, n, (hipStream_t)hip_stream);
+  if (err != hipSuccess) {
+    set_error(std::string("fe_zero_f32: ") + hipGetErrorString(err));
+    return FE_ERR_HIP;
+  }
+  return FE_OK;
+}
+
+extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
+                          int value_weighted, int score, float recency_decay, int64_t window, void* hip_stream) {
+  clear_error();
+  if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || (score && !importance)) {
+    set_error("fe_prefill: null pointer argument");
+    return FE_ERR_INVALID;
+  }
+  if (B < 1 || Hq < 1 || Hkv < 1 || N < 1 || D < 1 || Hq % Hkv != 0) {
+    set_error("fe_prefill: expected nonempty shapes with Hq divisible by Hkv");
+    return FE_ERR_INVALID;
+  }
+  if (D > 256) {
+    set_error("fe_prefill: head dimension must be <= 256");
+    return FE_ERR_INVALID;
+  }
+  if (dtype != FE_DTYPE_F16 && dtype != FE_DTYPE_BF16) {
+    set_error("fe_prefill: dtype must be FE_DTYPE_F16 or FE_DTYPE_BF16");
+    return FE_ERR_INVALID;
+  }
+  if (!isfinite(scale) || !isfinite(recency_decay) || recency_decay < 0.f) {
+    set_error("fe_prefill: scale must be finite and recency_decay finite and nonnegative");
+    return FE_ERR_INVALID;
+  }
+  if (window < 1 || window > N) {
+    set_error("fe_prefill: window must be the clamped observation window in [1, N]");
+    return FE_ERR_INVALID;
+  }
+  const int64_t G = Hq / Hkv;
+  const int64_t nqs = (N + 31) / 32;
+  const int64_t tiles_bh = G * nqs;
+  const int tpw = 1;
+  const int64_t wg_bh = (tiles_bh + 4 * tpw - 1) / (4 * tpw);
+  const int64_t blocks = B * Hkv * wg_bh;
+  if (N > (1LL << 30) || tiles_bh > (1LL << 30) || blocks > 0x7fffffffLL || B * Hkv > (1LL << 30)) {
+    set_error("fe_prefill: problem too large for one launch");
+    return FE_ERR_UNSUPPORTED;
+  }
+
+  AttnArgs a;
+  a.q = (const u16*)q;
+  a.k = (const u16*)k;
+  a.v = (const u16*)v;
+  a.out = (u16*)out;
+  a.imp = importance;
+  for (int i = 0; i < 4; ++i) {
+    a.qs[i] = q_strides[i];
+    a.ks[i] = k_strides[i];
+    a.vs[i] = v_strides[i];
+  }
+  a.N = (int)N;
+  a.D = (int)D;
+  a.G = (int)G;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.BH = (int)(B * Hkv);
+  a.tiles_bh = (int)tiles_bh;
+  a.wg_bh = (int)wg_bh;
+  const double log2e = 1.4426950408889634;
+  a.scale_log2 = (float)((double)scale * log2e);
+  a.abs_scale_log2 = fabsf(a.scale_log2);
+  a.neg_scale = a.scale_log2 < 0.f;
+  a.decay_log2 = (float)((double)recency_decay * log2e);
+  a.causal = causal ? 1 : 0;
+  a.score = score ? 1 : 0;
+  a.win_lo = (int)(N - window);
+  a.qvec = vec_ok(q, q_strides, D);
+  a.kvec = vec_ok(k, k_strides, D);
+  a.vvec = vec_ok(v, v_strides, D);
+  a.ovec = (D % 4 == 0) && (((uintptr_t)out & 7u) == 0);
+
+  int dpi = 0;
+  while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
+  FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
+
+  hipStream_t stream = (hipStream_t)hip_stream;
+  hipError_t err = hipSuccess;
+  {
+    std::lock_guard<std::mutex> lock(g_attr_mutex);
+    if (!ent.attr_set) {
+      err = hipFuncSetAttribute((const void*)ent.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ent.lds);
+      if (err != hipSuccess) {
+        set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
+        return FE_ERR_HIP;
+      }
+      ent.attr_set = true;
+    }
+  }
+  if (score) {
+    err = launch_zero_f32(importance, B * Hkv * N, stream);
+    if (err != hipSuccess) {
+      set_error(std::string("fe_prefill: zero-init launch: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+  }
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  const bool timed = fused_timing_enabled();
+  if (timed) {
+    if (hipEventCreate(&ev0) != hipSuccess || hipEventCreate(&ev1) != hipSuccess ||
+        hipEventRecord(ev0, stream) != hipSuccess) {
+      set_error("fe_prefill: timing event setup failed");
+      return FE_ERR_HIP;
+    }
+  }
+  void* kargs[] = {&a};
+  err = hipLaunchKernel((const void*)ent.fn, dim3((unsigned)blocks), dim3(256), kargs, ent.lds, stream);
+  if (err != hipSuccess) {
+    set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
+    return FE_ERR_HIP;
+  }
+  if (timed) {
+    if (hipEventRecord(ev1, stream) != hipSuccess) {
+      set_error("fe_prefill: timing event record failed");
+      return FE_ERR_HIP;
+    }
+    fused_timing_push(ev0, ev1);
+  }
+  if (score && value_weighted) {
+    const long long rows = B * Hkv * N;
+    const long long nb = (rows + 31) / 32;
+    if (dtype == FE_DTYPE_BF16)
+      hipLaunchKernelGGL(value_l1_scale_kernel<BF16>, dim3((unsigned)nb), dim3(256), 0, stream, (const u16*)v,
+                         (long long)v_strides[0], (long long)v_strides[1], (long long)v_strides[2],
+                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, a.vvec, importance, rows);
+    else
+      hipLaunchKernelGGL(value_l1_scale_kernel<F16>, dim3((unsigned)nb), dim3(256), 0, stream, (const u16*)v,
+                         (long long)v_strides[0], (long long)v_strides[1], (long long)v_strides[2],
+                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, a.vvec, importance, rows);
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+      set_error(std::string("fe_prefill: value-norm launch: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+  }
+  return FE_OK;
+}

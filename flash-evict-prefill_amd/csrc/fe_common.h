@@ -1,0 +1,66 @@
+// Shared device/host definitions for the flash_evict gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fe {
+
+typedef unsigned int u32;
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Element tags: storage is always 16-bit; the tag selects MFMA flavour and rounding.
+struct BF16 {
+  typedef __bf16 scalar;
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even pack of two floats (lo in bits 0..15).
+  static __device__ __forceinline__ u32 pack2(float lo, float hi) {
+    bf16x2 r = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
+    return __builtin_bit_cast(u32, r);
+  }
+  static __device__ __forceinline__ float to_f32(unsigned short bits) {
+    return __uint_as_float(((u32)bits) << 16);
+  }
+};
+
+struct F16 {
+  typedef _Float16 scalar;
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ u32 pack2(float lo, float hi) {
+    f16x2 r = __builtin_convertvector((f32x2){lo, hi}, f16x2);
+    return __builtin_bit_cast(u32, r);
+  }
+  static __device__ __forceinline__ float to_f32(unsigned short bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+};
+
+// max/sum of a value with its counterpart in the other 32-lane half of the wave.
+// v_permlane32_swap(x, x) returns {lanes 0-31: x[l], lanes 32-63: x[l-32]} and
+// {lanes 0-31: x[l+32], lanes 32-63: x[l]}; combining both halves is symmetric.
+__device__ __forceinline__ float half_swap_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+}  // namespace fe

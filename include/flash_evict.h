@@ -1,0 +1,113 @@
+/*
+ * flash_evict C ABI — MI355X (gfx950) prefill hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers, sizes and an opaque HIP
+ * stream, returns 0 on success and a negative code on failure (the message is then
+ * available from fe_last_error() on the calling thread). Nothing here throws, and
+ * nothing synchronises the stream: work is enqueued and the call returns.
+ *
+ * Reference interfaces replaced (paths are in anishesg/flash-evict-prefill):
+ *   fe_prefill        flash_evict/prefill.py:128-136  (importance zero-init + the Triton
+ *                     `_prefill[(cdiv(N,BM), B*Hq)](...)` launch, kernel at :14-83)
+ *   fe_zero_f32       flash_evict/prefill.py:129      (`torch.zeros` of the score array)
+ *   fe_select         flash_evict/prefill.py:160-169  (avg_pool1d, topk, tail arange/cat,
+ *                     sort, scatter_ of `select_tokens`), plus :180 (`~keep`) when invert=1
+ *   fe_select_host    the same `select_tokens` body for CPU tensors (tests call it on CPU,
+ *                     tests/test_prefill.py:77-84,149-159)
+ *   fe_kernel_resources  scripts/benchmark.py:104-111 (`_prefill.device_caches` resource dump)
+ */
+#ifndef FLASH_EVICT_H_
+#define FLASH_EVICT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of q/k/v/out. */
+enum { FE_DTYPE_F16 = 0, FE_DTYPE_BF16 = 1 };
+
+/* Error codes. */
+enum {
+  FE_OK = 0,
+  FE_ERR_INVALID = -1,     /* argument out of the supported range */
+  FE_ERR_HIP = -2,         /* a HIP runtime call failed */
+  FE_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+  FE_ERR_UNSUPPORTED = -4  /* shape/layout this build does not handle */
+};
+
+/*
+ * Fused prefill: attention output plus exact replay importance.
+ *
+ * q: [B,Hq,N,D], k/v: [B,Hkv,N,D], any element strides (qs/ks/vs = {b,h,n,d} strides in
+ * elements). out: contiguous [B,Hq,N,D] of the input dtype. importance: contiguous
+ * [B,Hkv,N] float32 (may be NULL when score == 0).
+ *
+ *   out[b,h,q,:]   = softmax_k(scale * q.k, causal)[q,:] @ v           (P rounded to the
+ *                    input dtype before P@V, FP32 accumulation)
+ *   importance[b,j,k] = ||v[b,j,k,:]||_1 (if value_weighted) *
+ *                    sum_{h in group j} sum_q w_q softmax(...)[b,h,q,k],
+ *   w_q = exp(recency_decay * (q - (N-1))) for q >= N - window, else 0.
+ *
+ * `window` is the already-clamped observation window: min(N, observation_window or N).
+ * The call zero-fills `importance` itself before accumulating into it.
+ * The attention output does not depend on score/window/value_weighted (bitwise).
+ */
+int fe_prefill(const void* q, const void* k, const void* v, void* out, float* importance,
+               int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+               const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+               int dtype, float scale, int causal, int value_weighted, int score,
+               float recency_decay, int64_t window, void* hip_stream);
+
+/* Zero-fill n floats with a fill kernel (graph-capture safe: no hipMemset node). */
+int fe_zero_f32(float* p, int64_t n, void* hip_stream);
+
+/*
+ * Token selection over `rows` score rows of length n (row r starts at
+ * scores + r * row_stride, unit element stride, float32).
+ *   past = row[:n-recent]; if pool_kernel > 1 and budget > recent, past is replaced by
+ *   avg_pool1d(past, pool_kernel, stride 1, pad pool_kernel/2, count_include_pad);
+ *   the (budget - recent) largest entries of past are kept (ties: lower index first),
+ *   together with the suffix [n-recent, n).
+ * indices_out: [rows, budget] int64, ascending. mask_out: [rows, n] bytes (0/1), the keep
+ * mask, or the eviction mask (1 = evict) when invert != 0. Either output may be NULL.
+ * workspace: device memory of at least fe_select_workspace_bytes(...) bytes (may be NULL
+ * when that is 0).
+ */
+size_t fe_select_workspace_bytes(int64_t rows, int64_t n, int64_t budget, int64_t recent,
+                                 int pool_kernel);
+int fe_select(const float* scores, int64_t rows, int64_t n, int64_t row_stride,
+              int64_t budget, int64_t recent, int pool_kernel,
+              int64_t* indices_out, uint8_t* mask_out, int invert,
+              void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* The same selection on host memory (CPU tensors); identical results to fe_select. */
+int fe_select_host(const float* scores, int64_t rows, int64_t n, int64_t row_stride,
+                   int64_t budget, int64_t recent, int pool_kernel,
+                   int64_t* indices_out, uint8_t* mask_out, int invert);
+
+/*
+ * Timing of the fused attention+score kernel alone: when enabled, fe_prefill records a
+ * HIP event pair around that kernel on the caller's stream. fe_fused_timing_read waits
+ * for the recorded events, returns the number of timed launches and their total
+ * duration in milliseconds, and clears the record.
+ */
+int fe_fused_timing_enable(int enable);
+int fe_fused_timing_read(int64_t* launches, double* total_ms);
+
+/* JSON description of the device kernels (registers, LDS, scratch), written to buf. */
+int fe_kernel_resources(char* buf, size_t cap);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* fe_last_error(void);
+
+/* ABI version (incremented on incompatible changes). */
+int fe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_EVICT_H_ */
