@@ -1,0 +1,196 @@
+"""Benchmark of the flash_evict prefill hot path on one MI355X.
+
+A step is one full `evict()` layer (zero-init, fused attention + replay-score kernel,
+value-norm scaling, radix top-k + mask) over resident synthetic bf16 inputs at the
+headline shape B=1, Hq=32, Hkv=8, N=32768, D=128, causal, budget 1024, recency_decay 0.1,
+reserved_recent 64, all-query replay (observation_window 0).
+
+Prints one JSON line on stdout:
+  value        = algorithmic attention+score TFLOP per layer / measured layer time
+  ms_per_step  = ms per layer (the metric's first half)
+  roofline     = the fused kernel alone: algorithmic TFLOP / its mean duration, timed with
+                 HIP events recorded by the library on the kernel's own stream
+  cpu_baseline = the CPU oracle (oracle/attention.chunked) on one query head of the same
+                 workload, extrapolated to the layer (reported only)
+Algorithmic work: 4*D*P_attn + 2*D*P_replay with P_attn = B*Hq*N(N+1)/2 (causal) and
+P_replay the (window-restricted) count of replayed query-key pairs.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "flash-evict-prefill_amd"), ROOT]
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+
+CONFIGS = {
+    # name: (B, Hq, Hkv, N, D, evict kwargs)
+    "headline": (1, 32, 8, 32768, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
+                                            observation_window=0, pool_kernel=1)),
+    "headline_b10": (1, 32, 8, 32768, 128, dict(budget=3277, recency_decay=0.0, reserved_recent=0,
+                                                observation_window=0, pool_kernel=1)),
+    "llama8k": (1, 32, 8, 8192, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
+                                          observation_window=0, pool_kernel=1)),
+    "qwen32k_w128": (1, 28, 4, 32768, 128, dict(budget=2048, recency_decay=0.0, reserved_recent=64,
+                                                observation_window=128, pool_kernel=5)),
+    "long131k": (1, 32, 8, 131072, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
+                                             observation_window=0, pool_kernel=1)),
+}
+
+
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_flop(b, hq, n, d, window, causal=True):
+    w = min(n, window or n)
+    if causal:
+        p_attn = b * hq * n * (n + 1) // 2
+        # sum_{q=n-w}^{n-1} (q+1)
+        p_replay = b * hq * (w * (2 * n - w + 1) // 2)
+    else:
+        p_attn = b * hq * n * n
+        p_replay = b * hq * w * n
+    return 4 * d * p_attn + 2 * d * p_replay
+
+
+def cpu_baseline(q, k, v, kw, threads):
+    """Time the CPU oracle on one query head (all N queries) and extrapolate to the layer."""
+    import torch
+    from oracle.attention import chunked
+    torch.set_num_threads(threads)
+    b, hq, n, d = q.shape
+    qc, kc, vc = q[:1, :1].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu()
+    args = dict(causal=True, value_weighted=True, recency_decay=kw["recency_decay"],
+                observation_window=kw["observation_window"], block=1024)
+    t0 = time.perf_counter()
+    chunked(qc, kc, vc, **args)
+    dt = time.perf_counter() - t0
+    heads = b * hq
+    layer_s = dt * heads
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"])
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": flop / layer_s / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_layer": layer_s * 1e3,
+        "cores": threads,
+        "kind": "port",
+        "sample": "oracle/attention.chunked (FP32 torch CPU, 1024-query blocks) on 1 of %d query heads "
+                  "(all %d queries, its KV head), %.2f s measured, x%d extrapolated; CPU %s"
+                  % (heads, n, dt, heads, cpu_model),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "fused_traffic.json"),
+                    help="rocprofv3 PMC summary giving HBM bytes per fused launch (optional)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the path shards by (batch, KV head) with "
+              "no exchange; multi-GPU runs are not part of it). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import flash_evict
+    from flash_evict import _lib
+
+    b, hq, hk, n, d, kw = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log("config %s: B=%d Hq=%d Hkv=%d N=%d D=%d %s" % (args.config, b, hq, hk, n, d, kw))
+    gen = torch.Generator(device=dev).manual_seed(20260910)
+    q = torch.randn((b, hq, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
+    k = torch.randn((b, hk, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
+    v = torch.randn((b, hk, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
+    torch.cuda.synchronize()
+
+    def step():
+        return flash_evict.evict(q, k, v, kw["budget"], reserved_recent=kw["reserved_recent"],
+                                 pool_kernel=kw["pool_kernel"], recency_decay=kw["recency_decay"],
+                                 observation_window=kw["observation_window"])
+
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            step()
+            torch.cuda.synchronize()
+            log("warmup %d/%d done" % (i + 1, args.warmup))
+        L = _lib.lib()
+        _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
+        _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        _lib.check(L.fe_fused_timing_enable(0), "fe_fused_timing_enable")
+        import ctypes
+        launches = ctypes.c_int64(0)
+        fused_ms = ctypes.c_double(0.0)
+        _lib.check(L.fe_fused_timing_read(ctypes.byref(launches), ctypes.byref(fused_ms)),
+                   "fe_fused_timing_read")
+    ms = elapsed * 1e3 / args.steps
+    log("timed %d steps: %.3f ms/layer" % (args.steps, ms))
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"])
+    fused_avg_ms = fused_ms.value / max(1, launches.value)
+    achieved = flop / (fused_avg_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(args.traffic_json):
+        try:
+            with open(args.traffic_json) as f:
+                tj = json.load(f)
+            if tj.get("config") == args.config:
+                traffic = tj.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    record = {
+        "metric": "ms/layer + fused attn+score TFLOP/s (% MFMA peak), N=32K Hq32/Hkv8 D128 bf16",
+        "value": round(flop / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v resident in HBM)",
+        "config": {"workload": "evict() layer, %s" % args.config, "B": b, "Hq": hq, "Hkv": hk, "N": n, "D": d,
+                   "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4)},
+        "roofline": {"bound": "mfma", "kernel": "fused_attn_score", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches.value},
+        "fused_share_of_layer": round(fused_avg_ms / ms, 4),
+    }
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        log("cpu baseline on %d threads ..." % threads)
+        record["cpu_baseline"] = cpu_baseline(q, k, v, kw, threads)
+    else:
+        record["cpu_baseline"] = None
+    print(json.dumps(record), flush=True)
+
+
+if __name__ == "__main__":
+    main()

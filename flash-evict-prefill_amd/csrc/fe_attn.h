@@ -1,0 +1,63 @@
+// Argument block and launch hooks shared by the fused attention + score kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "fe_common.h"
+
+namespace fe {
+
+typedef unsigned short u16;
+
+struct AttnArgs {
+  const u16* q;
+  const u16* k;
+  const u16* v;
+  u16* out;
+  float* imp;
+  long long qs[4], ks[4], vs[4];   // element strides {b, h, n, d}
+  int N, D, G, Hq, Hkv, BH;
+  int tiles_bh;                     // row tiles per (b, kv head): G * ceil(N/32)
+  int wg_bh;                        // workgroups per (b, kv head)
+  float scale_log2;                 // softmax scale * log2(e)
+  float abs_scale_log2;
+  float decay_log2;                 // recency_decay * log2(e)
+  int neg_scale;
+  int causal, score, win_lo;        // win_lo = N - W
+  int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
+};
+
+// Load 8 consecutive channels [d0, d0+8) of one row; zero beyond D.
+__device__ __forceinline__ u32x4 load8(const u16* row, long long sd, int d0, int D, int vec) {
+  if (vec) {
+    if (d0 < D) return *(const u32x4*)(row + d0);
+    return (u32x4){0u, 0u, 0u, 0u};
+  }
+  u32 w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int da = d0 + 2 * i, db = da + 1;
+    const u32 lo = da < D ? (u32)row[(long long)da * sd] : 0u;
+    const u32 hi = db < D ? (u32)row[(long long)db * sd] : 0u;
+    w[i] = lo | (hi << 16);
+  }
+  return (u32x4){w[0], w[1], w[2], w[3]};
+}
+
+// A launch plan: the kernel, its grid and dynamic LDS, and the rows per workgroup.
+struct FusedPlan {
+  const void* fn;
+  size_t lds;
+  int tpw;            // row tiles (32 queries of one head) per wave
+  const char* name;
+};
+
+// Fast path (fe_attn_fast.hip): D in {64, 128}, positive scale, 16-byte rows, buffer-
+// addressable K/V. Returns false (and leaves `plan` untouched) when it does not apply.
+bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan);
+hipError_t prepare_plan(const FusedPlan& plan);
+void append_fast_resources(std::string& out);
+
+}  // namespace fe

@@ -36,48 +36,11 @@
 #include <string>
 #include <vector>
 
-#include "fe_common.h"
+#include "fe_attn.h"
 #include "fe_internal.h"
 #include "../../include/flash_evict.h"
 
 namespace fe {
-
-typedef unsigned short u16;
-
-struct AttnArgs {
-  const u16* q;
-  const u16* k;
-  const u16* v;
-  u16* out;
-  float* imp;
-  long long qs[4], ks[4], vs[4];   // element strides {b, h, n, d}
-  int N, D, G, Hq, Hkv, BH;
-  int tiles_bh;                     // row tiles per (b, kv head): G * ceil(N/32)
-  int wg_bh;                        // workgroups per (b, kv head)
-  float scale_log2;                 // softmax scale * log2(e)
-  float abs_scale_log2;
-  float decay_log2;                 // recency_decay * log2(e)
-  int neg_scale;
-  int causal, score, win_lo;        // win_lo = N - W
-  int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
-};
-
-// Load 8 consecutive channels [d0, d0+8) of one row; zero beyond D.
-__device__ __forceinline__ u32x4 load8(const u16* row, long long sd, int d0, int D, int vec) {
-  if (vec) {
-    if (d0 < D) return *(const u32x4*)(row + d0);
-    return (u32x4){0u, 0u, 0u, 0u};
-  }
-  u32 w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int da = d0 + 2 * i, db = da + 1;
-    const u32 lo = da < D ? (u32)row[(long long)da * sd] : 0u;
-    const u32 hi = db < D ? (u32)row[(long long)db * sd] : 0u;
-    w[i] = lo | (hi << 16);
-  }
-  return (u32x4){w[0], w[1], w[2], w[3]};
-}
 
 template <int DP>
 struct Tile {
@@ -512,12 +475,11 @@ struct FusedEntry {
   FusedFn fn;
   size_t lds;
   const char* name;
-  bool attr_set;
 };
 
 template <typename E, int DP, int TPW>
 FusedEntry make_entry(const char* name) {
-  return FusedEntry{fused_attn_score_kernel<E, DP, TPW>, Tile<DP>::LDS, name, false};
+  return FusedEntry{fused_attn_score_kernel<E, DP, TPW>, Tile<DP>::LDS, name};
 }
 
 // Padded channel counts: D is rounded up to the next entry.
@@ -539,6 +501,7 @@ std::vector<FusedEntry>& fused_table() {
 }
 
 std::mutex g_attr_mutex;
+std::vector<const void*> g_attr_done;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -548,7 +511,17 @@ int vec_ok(const void* p, const int64_t* st, int64_t D) {
 
 }  // namespace
 
+hipError_t prepare_plan(const FusedPlan& plan) {
+  std::lock_guard<std::mutex> lock(g_attr_mutex);
+  for (const void* f : g_attr_done)
+    if (f == plan.fn) return hipSuccess;
+  hipError_t err = hipFuncSetAttribute(plan.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);
+  if (err == hipSuccess) g_attr_done.push_back(plan.fn);
+  return err;
+}
+
 void append_attn_resources(std::string& out) {
+  append_fast_resources(out);
   for (auto& e : fused_table()) {
     hipFuncAttributes attr;
     if (hipFuncGetAttributes(&attr, (const void*)e.fn) != hipSuccess) continue;
@@ -652,22 +625,22 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
   a.vvec = vec_ok(v, v_strides, D);
   a.ovec = (D % 4 == 0) && (((uintptr_t)out & 7u) == 0);
 
-  int dpi = 0;
-  while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
-  FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
+  FusedPlan plan;
+  if (!fast_plan(a, dtype, plan)) {
+    int dpi = 0;
+    while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
+    const FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
+    plan = FusedPlan{(const void*)ent.fn, ent.lds, 1, ent.name};
+  }
+  // Workgroups are sized by the plan's row tiles per wave.
+  a.wg_bh = (int)((tiles_bh + 4 * plan.tpw - 1) / (4 * plan.tpw));
+  const int64_t grid = B * Hkv * (int64_t)a.wg_bh;
 
   hipStream_t stream = (hipStream_t)hip_stream;
-  hipError_t err = hipSuccess;
-  {
-    std::lock_guard<std::mutex> lock(g_attr_mutex);
-    if (!ent.attr_set) {
-      err = hipFuncSetAttribute((const void*)ent.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ent.lds);
-      if (err != hipSuccess) {
-        set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
-        return FE_ERR_HIP;
-      }
-      ent.attr_set = true;
-    }
+  hipError_t err = prepare_plan(plan);
+  if (err != hipSuccess) {
+    set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
+    return FE_ERR_HIP;
   }
   if (score) {
     err = launch_zero_f32(importance, B * Hkv * N, stream);
@@ -686,7 +659,7 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
     }
   }
   void* kargs[] = {&a};
-  err = hipLaunchKernel((const void*)ent.fn, dim3((unsigned)blocks), dim3(256), kargs, ent.lds, stream);
+  err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(256), kargs, plan.lds, stream);
   if (err != hipSuccess) {
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;

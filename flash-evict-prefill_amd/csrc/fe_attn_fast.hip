@@ -1,0 +1,384 @@
+// Fast path of the fused prefill kernel for gfx950: D in {64, 128}, positive softmax scale,
+// 16-byte K/V rows. Same mathematics as the generic kernel in fe_attn.hip (reference
+// flash_evict/prefill.py:14-83); the differences are in data movement and scheduling:
+//
+//   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
+//     staging registers and no VALU work; rows past N read as zero through the buffer
+//     range check. LDS rows are stored unpadded with the 16-byte chunk index XOR-swizzled
+//     by the key, so fragment reads are bank-conflict free.
+//   * The A operand of O^T = V^T P^T (eight keys of one channel per lane) comes straight
+//     from the row-major V tile with two ds_read_b64_tr_b16 transposing reads; the key
+//     order of the read matches the S^T accumulator row order that becomes P^T.
+//   * Two LDS buffers per operand: the DMA for tile t+1 is in flight while tile t is
+//     computed, with one barrier per tile.
+//   * O is rescaled only when some row's running max actually rises (wave vote).
+//   * Masked logits are set to -inf in place, so masking costs one compare/select per
+//     element on diagonal and ragged tiles only.
+#include <math.h>
+#include <string>
+
+#include "fe_attn.h"
+#include "fe_internal.h"
+
+namespace fe {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <int DP>
+struct FastTile {
+  static constexpr int BN = 64;                  // keys per tile
+  static constexpr int CPR = DP / 8;             // 16-byte chunks per row
+  static constexpr int ROWB = DP * 2;            // bytes per row
+  static constexpr int TILE = BN * ROWB;         // bytes per K or V tile
+  static constexpr int DMA_PER_WAVE = (BN * CPR) / 256;
+  static constexpr int NDC = DP / 16;            // MFMA k-chunks of QK^T
+  static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
+  static constexpr size_t RED_OFF = 4 * (size_t)TILE;
+  static constexpr size_t LDS = RED_OFF + 2 * 4 * BN * 4;
+};
+
+// XOR applied to the 16-byte chunk index of row `key`: spreads the chunks that the 16
+// lanes of one LDS access phase read (same logical chunk, 16 consecutive keys) over all
+// 64 banks.
+template <int DP>
+__device__ __forceinline__ int swz(int key) {
+  return DP == 128 ? (key & 15) : ((key >> 1) & 7);
+}
+
+// Issue the DMA of one 64-key tile: wave wv moves blocks wv, wv+4, ... of 1 KB; lane l of a
+// block fills LDS chunk (block*64 + l) with the global chunk that the swizzle puts there.
+template <int DP>
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rs, unsigned char* tile, int kb, u32 rowb_g,
+                                         int wv, int lane) {
+  typedef FastTile<DP> T;
+#pragma unroll
+  for (int r = 0; r < T::DMA_PER_WAVE; ++r) {
+    const int blk = r * 4 + wv;
+    const int c = blk * 64 + lane;
+    const int key = c / T::CPR, pc = c % T::CPR;
+    const int lc = pc ^ swz<DP>(key);
+    const u32 voff = (u32)(kb + key) * rowb_g + (u32)lc * 16u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(tile + blk * 1024), 16, voff, 0, 0, 0);
+  }
+}
+
+template <int DP>
+__device__ __forceinline__ u32x4 k_frag(const unsigned char* tile, int key, int lc) {
+  return *(const u32x4*)(tile + key * FastTile<DP>::ROWB + ((lc ^ swz<DP>(key)) << 4));
+}
+
+// Eight keys of channel (32*dt + lane%32) in P^T slot order for 16-key chunk `kc0`:
+// slots 0-3 = keys kc0 + 4h + 0..3, slots 4-7 = keys kc0 + 8 + 4h + 0..3 (h = lane/32).
+template <int DP>
+__device__ __forceinline__ u32x4 v_frag(const unsigned char* tile, int kc0, int dt, int lane) {
+  const int r = lane & 15, g = lane >> 4, h = lane >> 5;
+  const int d = 32 * dt + 16 * (g & 1) + 4 * (r & 3);
+  const int lc = d >> 3, hb = (d >> 2) & 1;
+  const int k1 = kc0 + 4 * h + (r >> 2), k2 = k1 + 8;
+  const unsigned char* p1 = tile + k1 * FastTile<DP>::ROWB + ((lc ^ swz<DP>(k1)) << 4) + (hb << 3);
+  const unsigned char* p2 = tile + k2 * FastTile<DP>::ROWB + ((lc ^ swz<DP>(k2)) << 4) + (hb << 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(lds_ptr_t)p1);
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(lds_ptr_t)p2);
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return (u32x4){ua[0], ua[1], ub[0], ub[1]};
+}
+
+template <typename E, int DP, int TPW>
+__global__ __launch_bounds__(256, (TPW == 1 ? 2 : 1)) void fused_fast_kernel(const AttnArgs a) {
+  typedef FastTile<DP> T;
+  constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT;
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  constexpr float POS_INF = __builtin_huge_valf();
+
+  extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+  unsigned char* kt0 = smem;                     // K tiles [2]
+  unsigned char* vt0 = smem + 2 * T::TILE;       // V tiles [2]
+  float* red = (float*)(smem + T::RED_OFF);      // [2][4][BN]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hh = lane >> 5;
+  const int N = a.N;
+
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
+  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
+  const int t_begin = wg * 4 * TPW;
+  const int t_end = min(a.tiles_bh, t_begin + 4 * TPW);
+  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
+  const int kv_end = a.causal ? wg_q_hi : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  int q0[TPW], head[TPW], qlim[TPW];
+  bool tv[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = t_begin + wv * TPW + j;
+    tv[j] = t < t_end;
+    const int tt = tv[j] ? t : t_begin;
+    q0[j] = (tt / a.G) * 32;
+    head[j] = hkv * a.G + (tt - (tt / a.G) * a.G);
+    // last key this lane's query row may see; -1 for a padding tile
+    qlim[j] = !tv[j] ? -1 : (a.causal ? min(q0[j] + l32, N - 1) : N - 1);
+  }
+
+  u32x4 qf[TPW][NDC];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int qr = q0[j] + l32;
+    const bool ok = tv[j] && qr < N;
+    const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+#pragma unroll
+    for (int c = 0; c < NDC; ++c)
+      qf[j][c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
+  }
+
+  const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k + b * a.ks[0] + hkv * a.ks[1]), (short)0, (int)((u32)N * krow), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v + b * a.vs[0] + hkv * a.vs[1]), (short)0, (int)((u32)N * vrow), 0x00020000);
+
+  f32x16 o[TPW][NDT];
+  float m_run[TPW], l_run[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    m_run[j] = NEG_INF;
+    l_run[j] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = (f32x16){};
+  }
+
+  // ---------------- traversal 1
+  dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
+  dma_tile<DP>(vrs, vt0, 0, vrow, wv, lane);
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1;
+    const int kb = it * BN;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it + 1 < ntiles) {
+      dma_tile<DP>(krs, kt0 + (cur ^ 1) * T::TILE, kb + BN, krow, wv, lane);
+      dma_tile<DP>(vrs, vt0 + (cur ^ 1) * T::TILE, kb + BN, vrow, wv, lane);
+    }
+    const unsigned char* kt = kt0 + cur * T::TILE;
+    const unsigned char* vt = vt0 + cur * T::TILE;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kbs = kb + 32 * s;
+      bool act = false;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) act |= tv[j] && (!a.causal || kbs <= q0[j] + 31);
+      if (kbs >= kv_end || !act) continue;
+
+      f32x16 sacc[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) {
+        const u32x4 kf = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(kf, qf[j][c], sacc[j]);
+      }
+
+      u32x4 pb[TPW][2];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int wave_lim = !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1);
+        if (kbs + 31 > wave_lim) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kbs + 8 * (i >> 2) + 4 * hh + (i & 3);
+            sacc[j][i] = key <= qlim[j] ? sacc[j][i] : NEG_INF;
+          }
+        }
+        float mr = sacc[j][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mr = fmaxf(mr, sacc[j][i]);
+        mr = half_swap_max(mr);
+        const float mn = fmaxf(m_run[j], mr * a.scale_log2);
+        if (__any(mn > m_run[j])) {
+          const float corr = mn > m_run[j] ? fast_exp2(m_run[j] - mn) : 1.f;
+          l_run[j] *= corr;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) o[j][dt] *= corr;
+          m_run[j] = mn;
+        }
+        const float nm = m_run[j] == NEG_INF ? 0.f : -m_run[j];
+        float p[16];
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          p[i] = fast_exp2(fmaf(sacc[j][i], a.scale_log2, nm));
+          ps += p[i];
+        }
+        l_run[j] += ps;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+          pb[j][c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
+                              E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
+      }
+
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const u32x4 vf = v_frag<DP>(vt, 32 * s + 16 * c2, dt, lane);
+#pragma unroll
+          for (int j = 0; j < TPW; ++j) o[j][dt] = E::mfma(vf, pb[j][c2], o[j][dt]);
+        }
+      }
+    }
+  }
+
+  // ---------------- finish rows
+  float l_tot[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    l_tot[j] = half_swap_sum(l_run[j]);
+    const int qi = q0[j] + l32;
+    if (!tv[j] || qi >= N) continue;
+    const float inv = 1.f / l_tot[j];
+    u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * DP;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+        const u32 w0 = E::pack2(o[j][dt][4 * g4 + 0] * inv, o[j][dt][4 * g4 + 1] * inv);
+        const u32 w1 = E::pack2(o[j][dt][4 * g4 + 2] * inv, o[j][dt][4 * g4 + 3] * inv);
+        *(u32x2*)(op + d0) = (u32x2){w0, w1};
+      }
+    }
+  }
+
+  // ---------------- traversal 2: replay
+  if (!a.score || wg_q_hi - 1 < a.win_lo) return;
+
+  float bias[TPW][16];
+  bool rin[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int qi = q0[j] + l32;
+    const bool live = tv[j] && qi < N && qi >= a.win_lo;
+    const float br = live ? (m_run[j] + fast_log2(l_tot[j]) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bias[j][i] = __shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+    rin[j] = tv[j] && q0[j] + 31 >= a.win_lo;
+  }
+
+  float* imp_row = a.imp + (long long)bh * N;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every wave is done reading the traversal-1 tiles
+  dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1;
+    const int kb = it * BN;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it > 0 && tid < BN) {
+      // flush the previous tile's column sums (written before this barrier)
+      const float* rr = red + (cur ^ 1) * 4 * BN;
+      const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
+      const int key = kb - BN + tid;
+      if (sum != 0.f) unsafeAtomicAdd(imp_row + key, sum);
+    }
+    if (it + 1 < ntiles) dma_tile<DP>(krs, kt0 + (cur ^ 1) * T::TILE, kb + BN, krow, wv, lane);
+    const unsigned char* kt = kt0 + cur * T::TILE;
+    float cs[2] = {0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kbs = kb + 32 * s;
+      bool act = false;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) act |= rin[j] && (!a.causal || kbs <= q0[j] + 31);
+      if (kbs >= kv_end || !act) continue;
+      f32x16 sacc[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) {
+        const u32x4 kf = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
+      }
+      const int key = kbs + l32;
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        if (a.causal && kbs + 31 > q0[j]) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int qr = q0[j] + 8 * (i >> 2) + 4 * hh + (i & 3);
+            sacc[j][i] = key > qr ? NEG_INF : sacc[j][i];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cs[s] += fast_exp2(fmaf(sacc[j][i], a.scale_log2, -bias[j][i]));
+      }
+    }
+    cs[0] = half_swap_sum(cs[0]);
+    cs[1] = half_swap_sum(cs[1]);
+    if (hh == 0) {
+      float* rb = red + cur * 4 * BN + wv * BN;
+      rb[l32] = cs[0];
+      rb[32 + l32] = cs[1];
+    }
+  }
+  __syncthreads();
+  if (tid < BN) {
+    const int cur = (ntiles - 1) & 1;
+    const float* rr = red + cur * 4 * BN;
+    const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
+    const int key = (ntiles - 1) * BN + tid;
+    if (key < N && sum != 0.f) unsafeAtomicAdd(imp_row + key, sum);
+  }
+}
+
+namespace {
+
+template <typename E, int DP, int TPW>
+FusedPlan fast_entry(const char* name) {
+  return FusedPlan{(const void*)fused_fast_kernel<E, DP, TPW>, FastTile<DP>::LDS, TPW, name};
+}
+
+FusedPlan g_fast[] = {
+    fast_entry<F16, 64, 1>("fused_fast<f16,64,1>"),
+    fast_entry<F16, 128, 1>("fused_fast<f16,128,1>"),
+    fast_entry<BF16, 64, 1>("fused_fast<bf16,64,1>"),
+    fast_entry<BF16, 128, 1>("fused_fast<bf16,128,1>"),
+};
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool kv_ok(const void* p, const long long* st, int N, int D) {
+  if (st[3] != 1 || !aligned16(p) || st[0] % 8 || st[1] % 8 || st[2] % 8 || st[2] < D) return false;
+  // byte offsets of rows up to N + 64 (one tile past the end) must fit the 32-bit range
+  return (unsigned long long)(N + 64) * (unsigned long long)st[2] * 2ull < (1ull << 31);
+}
+
+}  // namespace
+
+bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
+  if (a.D != 64 && a.D != 128) return false;
+  if (!(a.scale_log2 > 0.f) || !a.qvec) return false;
+  if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
+  const int idx = (dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0);
+  plan = g_fast[idx];
+  return true;
+}
+
+void append_fast_resources(std::string& out) {
+  for (const auto& e : g_fast) {
+    hipFuncAttributes attr;
+    if (hipFuncGetAttributes(&attr, e.fn) != hipSuccess) continue;
+    char buf[512];
+    snprintf(buf, sizeof(buf),
+             "{\"kernel\":\"%s\",\"registers_per_thread\":%d,\"lds_static_bytes\":%zu,"
+             "\"lds_dynamic_bytes\":%zu,\"scratch_bytes_per_thread\":%zu,\"max_threads_per_block\":%d},",
+             e.name, attr.numRegs, (size_t)attr.sharedSizeBytes, e.lds, (size_t)attr.localSizeBytes,
+             attr.maxThreadsPerBlock);
+    out += buf;
+  }
+}
+
+}  // namespace fe
