@@ -55,24 +55,29 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
-def build(jobs=None, verbose=False):
-    """Compile every source and link the shared library. Returns the library path."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
+def build(jobs=None, verbose=False, out=None, defines=()):
+    """Compile every source and link the shared library. Returns the library path.
+
+    `out` overrides the library path and `defines` adds -D options (tuning variants).
+    """
+    build_dir = BUILD_DIR if not defines else os.path.join(BUILD_DIR, "_".join(defines).replace("=", ""))
+    os.makedirs(build_dir, exist_ok=True)
     hipcc = _hipcc()
+    dflags = ["-D" + d for d in defines]
     cmds, objs = [], []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD_DIR, src + ".o")
-        cmds.append([hipcc] + HIPCC_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
+        obj = os.path.join(build_dir, src + ".o")
+        cmds.append([hipcc] + HIPCC_FLAGS + dflags + ["-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     for src in CXX_SOURCES:
-        obj = os.path.join(BUILD_DIR, src + ".o")
+        obj = os.path.join(build_dir, src + ".o")
         cmds.append(["g++"] + CXX_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     t0 = time.time()
     jobs = jobs or min(len(cmds), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
-    out = os.path.join(OUT_DIR, LIB_NAME)
+    out = out or os.path.join(OUT_DIR, LIB_NAME)
     tmp = out + ".tmp"
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, out)
@@ -85,5 +90,7 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--out", default=None, help="library path (default: the package directory)")
+    ap.add_argument("-D", dest="defines", action="append", default=[], help="extra preprocessor define")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.out, tuple(args.defines)))

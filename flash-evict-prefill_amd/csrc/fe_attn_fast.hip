@@ -9,9 +9,12 @@
 //   * The A operand of O^T = V^T P^T (eight keys of one channel per lane) comes straight
 //     from the row-major V tile with two ds_read_b64_tr_b16 transposing reads; the key
 //     order of the read matches the S^T accumulator row order that becomes P^T.
-//   * Two LDS buffers per operand: the DMA for tile t+1 is in flight while tile t is
-//     computed, with one barrier per tile.
-//   * O is rescaled only when some row's running max actually rises (wave vote).
+//   * Two LDS buffers per operand with K one tile ahead of V: iteration t issues the MFMAs
+//     of QK(t+1) before the softmax VALU work of tile t (and, in the replay, before the
+//     exp/column sums of tile t), so matrix and vector work of one wave can overlap; one
+//     barrier per 64-key tile.
+//   * O is rescaled only when some row's max exceeds the running reference by more than
+//     2^8 (wave vote), so rescaling is rare after the first tiles.
 //   * Masked logits are set to -inf in place, so masking costs one compare/select per
 //     element on diagonal and ragged tiles only.
 #include <math.h>
@@ -23,7 +26,30 @@
 namespace fe {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Raise the wave's issue priority around MFMA blocks so that, of the two waves sharing a
+// SIMD, the one with matrix work ready issues it first while the other fills the MFMA
+// shadow with its softmax VALU work.
+#ifndef FE_SETPRIO
+#define FE_SETPRIO 1
+#endif
+// FE_PIPELINE=1 selects the software-pipelined schedule (QK of the next tile issued before
+// the softmax of the current one); 0 the per-tile schedule.
+#ifndef FE_PIPELINE
+#define FE_PIPELINE 0
+#endif
+#if FE_SETPRIO
+#define FE_PRIO_HI() __builtin_amdgcn_s_setprio(1)
+#define FE_PRIO_LO() __builtin_amdgcn_s_setprio(0)
+#else
+#define FE_PRIO_HI() ((void)0)
+#define FE_PRIO_LO() ((void)0)
+#endif
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Threshold (log2 units) by which a row's max must exceed the running reference max
+// before O and l are rescaled.
+constexpr float RESCALE_LOG2 = 8.f;
 
 template <int DP>
 struct FastTile {
@@ -38,12 +64,17 @@ struct FastTile {
   static constexpr size_t LDS = RED_OFF + 2 * 4 * BN * 4;
 };
 
-// XOR applied to the 16-byte chunk index of row `key`: spreads the chunks that the 16
-// lanes of one LDS access phase read (same logical chunk, 16 consecutive keys) over all
-// 64 banks.
+// XOR applied to the 16-byte chunk index of row `key`. Two read patterns must be bank-
+// conflict free (64 banks x 4 B = 256 B per cycle):
+//   K fragments: 16 consecutive keys, one logical chunk per access phase;
+//   V transposing reads: 4 consecutive keys x 4 consecutive chunks (aligned group of 4).
+// Moving the key's two low bits into the chunk's high bits serves both: the 16 keys map to
+// 16 distinct chunks, and the 4 keys of a transposing read land in 4 different chunk
+// groups. For 128-byte rows (D = 64) two rows share a bank cycle, so key bit 0 selects the
+// half and bits 1..3 are spread the same way.
 template <int DP>
 __device__ __forceinline__ int swz(int key) {
-  return DP == 128 ? (key & 15) : ((key >> 1) & 7);
+  return DP == 128 ? (((key & 3) << 2) | ((key >> 2) & 3)) : ((((key >> 1) & 1) << 2) | ((key >> 2) & 3));
 }
 
 // Issue the DMA of one 64-key tile: wave wv moves blocks wv, wv+4, ... of 1 KB; lane l of a
@@ -150,86 +181,181 @@ __global__ __launch_bounds__(256, (TPW == 1 ? 2 : 1)) void fused_fast_kernel(con
   }
 
   // ---------------- traversal 1
+  // Largest key any row of this wave attends to, and the smallest per-row limit of each
+  // row tile (lane 0's): tiles past wave_hi are skipped, tiles past lo_lim[j] are masked.
+  int lo_lim[TPW];
+  int wave_hi = -1;
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    lo_lim[j] = !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1);
+    if (tv[j]) wave_hi = max(wave_hi, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
+  }
+
+  // S^T = K Q^T for the 64 keys of one tile (two 32-key accumulators per row tile): per
+  // 32-key half, the eight K fragments are requested, then the MFMA chain issues at raised
+  // priority.
+  auto qk_tile = [&](const unsigned char* kt, f32x16 (&sacc)[TPW][2]) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 kf[NDC];
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) kf[c] = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
+      FE_PRIO_HI();
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        sacc[j][s] = E::mfma(kf[0], qf[j][0], (f32x16){});
+#pragma unroll
+        for (int c = 1; c < NDC; ++c) sacc[j][s] = E::mfma(kf[c], qf[j][c], sacc[j][s]);
+      }
+      FE_PRIO_LO();
+    }
+  };
+
+  // Mask, running max over the 64 keys of one tile, rescale of O and l when needed.
+  // Returns nothing; leaves -m_run (0 for a row with no key yet) in nm.
+  auto tile_stats = [&](int kb, f32x16 (&sacc)[TPW][2], float (&nm)[TPW]) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      if (kb + BN - 1 > lo_lim[j]) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb + 32 * s + 8 * (i >> 2) + 4 * hh + (i & 3);
+            sacc[j][s][i] = key <= qlim[j] ? sacc[j][s][i] : NEG_INF;
+          }
+      }
+      // max over the 32 keys of this lane: four independent max chains, then a tree
+      float m4[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        m4[t] = fmaxf(sacc[j][0][4 * t], sacc[j][1][4 * t]);
+#pragma unroll
+        for (int i = 1; i < 4; ++i) m4[t] = fmaxf(m4[t], fmaxf(sacc[j][0][4 * t + i], sacc[j][1][4 * t + i]));
+      }
+      float mr = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      mr = half_swap_max(mr);
+      // The reference max only moves when a row's max exceeds it by more than 2^RESCALE_LOG2
+      // (P <= 2^8 stays exact enough in bf16/fp16 and O/l is unchanged), so O is rescaled
+      // on a handful of tiles per row instead of on every new maximum.
+      const float mt = mr * a.scale_log2;
+      if (__any(mt > m_run[j] + RESCALE_LOG2)) {
+        const float mn = fmaxf(m_run[j], mt);
+        const float corr = mn > m_run[j] ? fast_exp2(m_run[j] - mn) : 1.f;
+        l_run[j] *= corr;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[j][dt] *= corr;
+        m_run[j] = mn;
+      }
+      nm[j] = m_run[j] == NEG_INF ? 0.f : -m_run[j];
+    }
+  };
+
+  // P = exp2(S*scale - m) rounded to the input dtype (packed as the B operand of P@V)
+  auto tile_exp = [&](f32x16 (&sacc)[TPW][2], const float (&nm)[TPW], u32x4 (&pb)[TPW][4]) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      float ps4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          p[i] = fast_exp2(fmaf(sacc[j][s][i], a.scale_log2, nm[j]));
+          ps4[i & 3] += p[i];
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+          pb[j][2 * s + c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
+                                      E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
+      }
+      l_run[j] += (ps4[0] + ps4[1]) + (ps4[2] + ps4[3]);
+    }
+  };
+
+  // O^T += V^T P^T over the four 16-key chunks of one tile, one 32-channel tile of O^T
+  // at a time (four V fragments requested, then four MFMAs at raised priority)
+  auto pv_tile = [&](const unsigned char* vt, const u32x4 (&pb)[TPW][4]) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      u32x4 vf[4];
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) vf[c4] = v_frag<DP>(vt, 16 * c4, dt, lane);
+      FE_PRIO_HI();
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) o[j][dt] = E::mfma(vf[c4], pb[j][c4], o[j][dt]);
+      FE_PRIO_LO();
+    }
+  };
+
+#if FE_PIPELINE
+  // Pipeline: K runs one tile ahead of V in the two-buffer rings. Iteration t waits for
+  // K(t+1) and V(t), starts the DMA of K(t+2) and V(t+1) into the buffers iteration t-1
+  // finished with, settles the statistics of tile t, then issues QK(t+1) interleaved
+  // (one LDS read, one MFMA, several VALU ops at a time) with the exponentials of tile t,
+  // and finally P@V of tile t.
+  f32x16 sA[TPW][2], sB[TPW][2];
+  dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
+  dma_tile<DP>(vrs, vt0, 0, vrow, wv, lane);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (ntiles > 1) dma_tile<DP>(krs, kt0 + T::TILE, BN, krow, wv, lane);
+  if (wave_hi >= 0) qk_tile(kt0, sA);
+
+  auto t1_step = [&](int it, f32x16 (&cur)[TPW][2], f32x16 (&nxt)[TPW][2]) {
+    const int kb = it * BN;
+    const int buf = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it + 2 < ntiles) dma_tile<DP>(krs, kt0 + buf * T::TILE, kb + 2 * BN, krow, wv, lane);
+    if (it + 1 < ntiles) dma_tile<DP>(vrs, vt0 + (buf ^ 1) * T::TILE, kb + BN, vrow, wv, lane);
+    if (kb > wave_hi) return;
+    float nm[TPW];
+    tile_stats(kb, cur, nm);
+    // Branch-free region: QK(t+1) (the last tile reads a stale buffer whose result is
+    // never used) interleaved with the exponentials of tile t.
+    u32x4 pb[TPW][4];
+    qk_tile(kt0 + (buf ^ 1) * T::TILE, nxt);
+    tile_exp(cur, nm, pb);
+#pragma unroll
+    for (int g = 0; g < 2 * NDC * TPW; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+    }
+    pv_tile(vt0 + buf * T::TILE, pb);
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    t1_step(it, sA, sB);
+    if (it + 1 < ntiles) t1_step(it + 1, sB, sA);
+  }
+#else
+  // Per tile: wait for K(t) and V(t), start the DMA of tile t+1 into the other buffers,
+  // QK(t), statistics, exponentials, P@V(t). The two waves sharing a SIMD overlap each
+  // other's MFMA and VALU phases; s_setprio favours the one with matrix work ready.
   dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
   dma_tile<DP>(vrs, vt0, 0, vrow, wv, lane);
   for (int it = 0; it < ntiles; ++it) {
-    const int cur = it & 1;
     const int kb = it * BN;
+    const int buf = it & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (it + 1 < ntiles) {
-      dma_tile<DP>(krs, kt0 + (cur ^ 1) * T::TILE, kb + BN, krow, wv, lane);
-      dma_tile<DP>(vrs, vt0 + (cur ^ 1) * T::TILE, kb + BN, vrow, wv, lane);
+      dma_tile<DP>(krs, kt0 + (buf ^ 1) * T::TILE, kb + BN, krow, wv, lane);
+      dma_tile<DP>(vrs, vt0 + (buf ^ 1) * T::TILE, kb + BN, vrow, wv, lane);
     }
-    const unsigned char* kt = kt0 + cur * T::TILE;
-    const unsigned char* vt = vt0 + cur * T::TILE;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int kbs = kb + 32 * s;
-      bool act = false;
-#pragma unroll
-      for (int j = 0; j < TPW; ++j) act |= tv[j] && (!a.causal || kbs <= q0[j] + 31);
-      if (kbs >= kv_end || !act) continue;
-
-      f32x16 sacc[TPW];
-#pragma unroll
-      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
-#pragma unroll
-      for (int c = 0; c < NDC; ++c) {
-        const u32x4 kf = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(kf, qf[j][c], sacc[j]);
-      }
-
-      u32x4 pb[TPW][2];
-#pragma unroll
-      for (int j = 0; j < TPW; ++j) {
-        const int wave_lim = !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1);
-        if (kbs + 31 > wave_lim) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kbs + 8 * (i >> 2) + 4 * hh + (i & 3);
-            sacc[j][i] = key <= qlim[j] ? sacc[j][i] : NEG_INF;
-          }
-        }
-        float mr = sacc[j][0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) mr = fmaxf(mr, sacc[j][i]);
-        mr = half_swap_max(mr);
-        const float mn = fmaxf(m_run[j], mr * a.scale_log2);
-        if (__any(mn > m_run[j])) {
-          const float corr = mn > m_run[j] ? fast_exp2(m_run[j] - mn) : 1.f;
-          l_run[j] *= corr;
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) o[j][dt] *= corr;
-          m_run[j] = mn;
-        }
-        const float nm = m_run[j] == NEG_INF ? 0.f : -m_run[j];
-        float p[16];
-        float ps = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          p[i] = fast_exp2(fmaf(sacc[j][i], a.scale_log2, nm));
-          ps += p[i];
-        }
-        l_run[j] += ps;
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2)
-          pb[j][c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
-                              E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
-      }
-
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const u32x4 vf = v_frag<DP>(vt, 32 * s + 16 * c2, dt, lane);
-#pragma unroll
-          for (int j = 0; j < TPW; ++j) o[j][dt] = E::mfma(vf, pb[j][c2], o[j][dt]);
-        }
-      }
-    }
+    if (kb > wave_hi) continue;
+    f32x16 sacc[TPW][2];
+    qk_tile(kt0 + buf * T::TILE, sacc);
+    float nm[TPW];
+    tile_stats(kb, sacc, nm);
+    u32x4 pb[TPW][4];
+    tile_exp(sacc, nm, pb);
+    pv_tile(vt0 + buf * T::TILE, pb);
   }
+#endif
 
   // ---------------- finish rows
   float l_tot[TPW];
@@ -257,6 +383,7 @@ __global__ __launch_bounds__(256, (TPW == 1 ? 2 : 1)) void fused_fast_kernel(con
 
   float bias[TPW][16];
   bool rin[TPW];
+  int wave_hi_r = -1;
 #pragma unroll
   for (int j = 0; j < TPW; ++j) {
     const int qi = q0[j] + l32;
@@ -265,69 +392,138 @@ __global__ __launch_bounds__(256, (TPW == 1 ? 2 : 1)) void fused_fast_kernel(con
 #pragma unroll
     for (int i = 0; i < 16; ++i) bias[j][i] = __shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
     rin[j] = tv[j] && q0[j] + 31 >= a.win_lo;
+    if (rin[j]) wave_hi_r = max(wave_hi_r, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
   }
 
   float* imp_row = a.imp + (long long)bh * N;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();  // every wave is done reading the traversal-1 tiles
-  dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
-  for (int it = 0; it < ntiles; ++it) {
-    const int cur = it & 1;
-    const int kb = it * BN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (it > 0 && tid < BN) {
-      // flush the previous tile's column sums (written before this barrier)
-      const float* rr = red + (cur ^ 1) * 4 * BN;
-      const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
-      const int key = kb - BN + tid;
-      if (sum != 0.f) unsafeAtomicAdd(imp_row + key, sum);
-    }
-    if (it + 1 < ntiles) dma_tile<DP>(krs, kt0 + (cur ^ 1) * T::TILE, kb + BN, krow, wv, lane);
-    const unsigned char* kt = kt0 + cur * T::TILE;
-    float cs[2] = {0.f, 0.f};
+
+  // S = Q K^T (lanes hold keys) for the 64 keys of one tile
+  auto qk_replay = [&](const unsigned char* kt, f32x16 (&sacc)[TPW][2]) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int kbs = kb + 32 * s;
-      bool act = false;
+      u32x4 kf[NDC];
 #pragma unroll
-      for (int j = 0; j < TPW; ++j) act |= rin[j] && (!a.causal || kbs <= q0[j] + 31);
-      if (kbs >= kv_end || !act) continue;
-      f32x16 sacc[TPW];
-#pragma unroll
-      for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
-#pragma unroll
-      for (int c = 0; c < NDC; ++c) {
-        const u32x4 kf = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
-      }
-      const int key = kbs + l32;
+      for (int c = 0; c < NDC; ++c) kf[c] = k_frag<DP>(kt, 32 * s + l32, 2 * c + hh);
+      FE_PRIO_HI();
 #pragma unroll
       for (int j = 0; j < TPW; ++j) {
-        if (a.causal && kbs + 31 > q0[j]) {
+        sacc[j][s] = E::mfma(qf[j][0], kf[0], (f32x16){});
+#pragma unroll
+        for (int c = 1; c < NDC; ++c) sacc[j][s] = E::mfma(qf[j][c], kf[c], sacc[j][s]);
+      }
+      FE_PRIO_LO();
+    }
+  };
+
+  // Column sums of one tile's S (in `cur`) -> cs[2]; diagonal tiles are masked first.
+  auto replay_sums = [&](int kb, f32x16 (&cur)[TPW][2], float (&cs)[2]) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float c4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c4[i & 3] += fast_exp2(fmaf(cur[j][s][i], a.scale_log2, -bias[j][i]));
+        cs[s] += (c4[0] + c4[1]) + (c4[2] + c4[3]);
+      }
+    }
+  };
+  auto replay_mask = [&](int kb, f32x16 (&cur)[TPW][2]) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+      if (a.causal && kb + BN - 1 > q0[j]) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int key = kb + 32 * s + l32;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int qr = q0[j] + 8 * (i >> 2) + 4 * hh + (i & 3);
-            sacc[j][i] = key > qr ? NEG_INF : sacc[j][i];
+            cur[j][s][i] = key > qr ? NEG_INF : cur[j][s][i];
           }
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) cs[s] += fast_exp2(fmaf(sacc[j][i], a.scale_log2, -bias[j][i]));
       }
     }
+  };
+  // Flush of the previous tile's four per-wave column sums (written before the barrier
+  // that precedes this call): one atomic per key per workgroup.
+  auto replay_flush = [&](int kb_prev, int buf_prev) {
+    if (tid < BN) {
+      const float* rr = red + buf_prev * 4 * BN;
+      const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
+      const int key = kb_prev + tid;
+      if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+    }
+  };
+  auto replay_store = [&](int buf, float (&cs)[2]) {
     cs[0] = half_swap_sum(cs[0]);
     cs[1] = half_swap_sum(cs[1]);
     if (hh == 0) {
-      float* rb = red + cur * 4 * BN + wv * BN;
+      float* rb = red + buf * 4 * BN + wv * BN;
       rb[l32] = cs[0];
       rb[32 + l32] = cs[1];
     }
+  };
+
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every wave is done reading the traversal-1 tiles
+  dma_tile<DP>(krs, kt0, 0, krow, wv, lane);
+#if FE_PIPELINE
+  // Same pipeline as traversal 1 with K only: QK(t+1) is interleaved with the exp/column
+  // sums of tile t.
+  f32x16 rA[TPW][2], rB[TPW][2];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (ntiles > 1) dma_tile<DP>(krs, kt0 + T::TILE, BN, krow, wv, lane);
+  if (wave_hi_r >= 0) qk_replay(kt0, rA);
+
+  auto t2_step = [&](int it, f32x16 (&cur)[TPW][2], f32x16 (&nxt)[TPW][2]) {
+    const int kb = it * BN;
+    const int buf = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it > 0) replay_flush(kb - BN, buf ^ 1);
+    if (it + 2 < ntiles) dma_tile<DP>(krs, kt0 + buf * T::TILE, kb + 2 * BN, krow, wv, lane);
+    float cs[2] = {0.f, 0.f};
+    if (kb <= wave_hi_r) {
+      replay_mask(kb, cur);
+      // Branch-free region: QK(t+1) interleaved with the exp/column sums of tile t.
+      qk_replay(kt0 + (buf ^ 1) * T::TILE, nxt);
+      replay_sums(kb, cur, cs);
+#pragma unroll
+      for (int g = 0; g < 2 * NDC * TPW; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+      }
+    }
+    replay_store(buf, cs);
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    t2_step(it, rA, rB);
+    if (it + 1 < ntiles) t2_step(it + 1, rB, rA);
   }
+#else
+  for (int it = 0; it < ntiles; ++it) {
+    const int kb = it * BN;
+    const int buf = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it > 0) replay_flush(kb - BN, buf ^ 1);
+    if (it + 1 < ntiles) dma_tile<DP>(krs, kt0 + (buf ^ 1) * T::TILE, kb + BN, krow, wv, lane);
+    float cs[2] = {0.f, 0.f};
+    if (kb <= wave_hi_r) {
+      f32x16 cur[TPW][2];
+      qk_replay(kt0 + buf * T::TILE, cur);
+      replay_mask(kb, cur);
+      replay_sums(kb, cur, cs);
+    }
+    replay_store(buf, cs);
+  }
+#endif
   __syncthreads();
   if (tid < BN) {
-    const int cur = (ntiles - 1) & 1;
-    const float* rr = red + cur * 4 * BN;
+    const int buf = (ntiles - 1) & 1;
+    const float* rr = red + buf * 4 * BN;
     const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
     const int key = (ntiles - 1) * BN + tid;
     if (key < N && sum != 0.f) unsafeAtomicAdd(imp_row + key, sum);

@@ -9,7 +9,8 @@ import os
 import threading
 
 LIB_NAME = "libflash_evict_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# FLASH_EVICT_LIB may name another build of the same library (e.g. a tuning variant).
+LIB_PATH = os.environ.get("FLASH_EVICT_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 FE_DTYPE_F16 = 0
 FE_DTYPE_BF16 = 1
