@@ -13,8 +13,7 @@
 //     of QK(t+1) before the softmax VALU work of tile t (and, in the replay, before the
 //     exp/column sums of tile t), so matrix and vector work of one wave can overlap; one
 //     barrier per 64-key tile.
-//   * O is rescaled only when some row's max exceeds the running reference by more than
-//     2^8 (wave vote), so rescaling is rare after the first tiles.
+//   * O is rescaled only when some row's running max actually rises (wave vote).
 //   * Masked logits are set to -inf in place, so masking costs one compare/select per
 //     element on diagonal and ragged tiles only.
 #include <math.h>
@@ -47,9 +46,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 #endif
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// Threshold (log2 units) by which a row's max must exceed the running reference max
-// before O and l are rescaled.
-constexpr float RESCALE_LOG2 = 8.f;
 
 template <int DP>
 struct FastTile {
@@ -235,11 +231,11 @@ __global__ __launch_bounds__(256, (TPW == 1 ? 2 : 1)) void fused_fast_kernel(con
       }
       float mr = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
       mr = half_swap_max(mr);
-      // The reference max only moves when a row's max exceeds it by more than 2^RESCALE_LOG2
-      // (P <= 2^8 stays exact enough in bf16/fp16 and O/l is unchanged), so O is rescaled
-      // on a handful of tiles per row instead of on every new maximum.
+      // Exact running max: the dominant probability of a row stays exactly 1 before it is
+      // rounded to the input dtype (a stale max would cost up to 2^-9 relative error on the
+      // term that dominates a peaked row). O and l are only touched when some row's max rose.
       const float mt = mr * a.scale_log2;
-      if (__any(mt > m_run[j] + RESCALE_LOG2)) {
+      if (__any(mt > m_run[j])) {
         const float mn = fmaxf(m_run[j], mt);
         const float corr = mn > m_run[j] ? fast_exp2(m_run[j] - mn) : 1.f;
         l_run[j] *= corr;

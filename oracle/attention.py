@@ -42,11 +42,15 @@ def materialized(q, k, v, *, causal=True, value_weighted=True, scale=None,
 
 
 def chunked(q, k, v, *, causal=True, value_weighted=True, scale=None,
-            recency_decay=0., observation_window=0, block=1024, heads=None, want_out=True):
+            recency_decay=0., observation_window=0, block=1024, heads=None, want_out=True,
+            query_rows=None):
     """Exact FP32 oracle streamed over (head, query block); never forms the N x N matrix.
 
     `heads` optionally restricts the computation to a list of (b, query head) pairs (the
-    importance then only holds their contributions). Returns (out or None, mass).
+    importance then only holds their contributions). `query_rows`, a list of (q0, q1)
+    ranges, restricts the output rows computed (only those rows of `out` are filled; the
+    importance is then only meaningful when every weighted row is included).
+    Returns (out or None, mass).
     """
     b, hq, n, d = q.shape
     hk = k.shape[1]
@@ -62,8 +66,11 @@ def chunked(q, k, v, *, causal=True, value_weighted=True, scale=None,
         kf = k[bi, j].float()
         vf = v[bi, j].float()
         col = torch.zeros(n, dtype=torch.float32, device=q.device)
-        for q0 in range(0, n, block):
-            q1 = min(n, q0 + block)
+        if query_rows is None:
+            spans = [(q0, min(n, q0 + block)) for q0 in range(0, n, block)]
+        else:
+            spans = [(a, min(hi_, a + block)) for lo_, hi_ in query_rows for a in range(lo_, hi_, block)]
+        for q0, q1 in spans:
             if not want_out and q1 <= win_lo:
                 continue
             kend = q1 if causal else n

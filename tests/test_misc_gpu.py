@@ -1,0 +1,118 @@
+"""GPU checks beyond the reference tests: argument validation on device tensors, the generic
+kernel's layouts and scales, golden fixtures, determinism, and resource introspection."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import flash_evict
+from flash_evict import prefill
+from oracle.attention import materialized
+from _helpers import seeded_randn
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _qkv(b=1, hq=4, hk=2, n=96, d=64, dtype=torch.bfloat16, seed=3):
+    return (seeded_randn((b, hq, n, d), dtype, seed), seeded_randn((b, hk, n, d), dtype, seed + 1),
+            seeded_randn((b, hk, n, d), dtype, seed + 2))
+
+
+def test_argument_validation_on_device():
+    # flash_evict/prefill.py:117-126 of the reference
+    q, k, v = _qkv()
+    for kw in (dict(recency_decay=-1.0), dict(recency_decay=float("inf")), dict(observation_window=-1),
+               dict(observation_window=True), dict(observation_window=2.0), dict(block_q=48),
+               dict(block_k=16), dict(scale=float("nan"))):
+        with pytest.raises(ValueError):
+            prefill(q, k, v, **kw)
+    qg = q.clone().requires_grad_(True)
+    with pytest.raises(ValueError, match="Inference only"):
+        prefill(qg, k, v)
+    with torch.no_grad():
+        prefill(qg, k, v)
+    with pytest.raises(ValueError, match="same device and dtype"):
+        prefill(q, k.half(), v)
+    with pytest.raises(ValueError, match="fp16 or bf16"):
+        prefill(q.float(), k.float(), v.float())
+    for bq in (16, 32, 64):
+        for bk in (32, 64, 128):
+            out, _ = prefill(q, k, v, block_q=bq, block_k=bk)   # accepted tile hints, same result
+            assert torch.equal(out, prefill(q, k, v)[0])
+
+
+@pytest.mark.parametrize("d", [16, 32, 80, 100, 136, 200, 256])
+def test_generic_head_dims(d):
+    print(f"generic head dim {d}", flush=True)
+    q, k, v = _qkv(hq=4, hk=1, n=150, d=d, dtype=torch.float16, seed=d)
+    out, imp = prefill(q, k, v, recency_decay=0.05)
+    ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), recency_decay=0.05)
+    torch.testing.assert_close(out.float().cpu(), ref_out, atol=2e-3, rtol=6e-3)
+    torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+@pytest.mark.parametrize("scale", [-0.1, 0.0, 0.5, 3.0])
+def test_scales(scale):
+    q, k, v = _qkv(n=130, d=64, seed=11)
+    for causal in (True, False):
+        out, imp = prefill(q, k, v, scale=scale, causal=causal)
+        ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), scale=scale, causal=causal)
+        torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+        torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+def test_unusual_layouts():
+    # channel stride != 1 (D not innermost) and unaligned views take the generic loaders
+    g = torch.Generator().manual_seed(4)
+    base = torch.randn(1, 64, 70, 4, generator=g).to(torch.bfloat16).cuda()    # [B, D, N, H]
+    q = base.permute(0, 3, 2, 1)                                                  # [B, H, N, D], d-stride 280
+    kb = torch.randn(1, 2, 70, 65, generator=g).to(torch.bfloat16).cuda()
+    k, v = kb[..., 1:], kb.flip(-1)[..., 1:]                                      # offset / negative-free views
+    assert q.stride(-1) != 1 and k.data_ptr() % 16 != 0
+    out, imp = prefill(q, k, v)
+    ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu())
+    torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+    torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+    # broadcast K/V along tokens (stride 0) must not use the buffer-addressed fast path
+    k0 = torch.randn(1, 2, 1, 64, generator=g).to(torch.bfloat16).cuda().expand(1, 2, 70, 64)
+    assert k0.data_ptr() % 16 == 0 and k0.stride(2) == 0
+    out, imp = prefill(q.contiguous(), k0, k0)
+    ref_out, ref_imp = materialized(q.cpu(), k0.cpu(), k0.cpu())
+    torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+    torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+def test_golden_fixtures():
+    data = np.load(os.path.join(GOLDEN, "prefill_small.npz"), allow_pickle=False)
+    for name in sorted({f.split(".")[0] for f in data.files}):
+        meta = json.loads(str(data[f"{name}.meta"]))
+        dt = getattr(torch, meta["dtype"])
+        q, k, v = (torch.from_numpy(data[f"{name}.{t}"]).view(dt).cuda() for t in "qkv")
+        out, imp = prefill(q, k, v, **meta["kwargs"])
+        atol = 1.2e-2 if dt == torch.bfloat16 else 2e-3
+        torch.testing.assert_close(out.float().cpu(), torch.from_numpy(data[f"{name}.out"]), atol=atol, rtol=6e-3)
+        torch.testing.assert_close(imp.cpu(), torch.from_numpy(data[f"{name}.importance"]), atol=3e-5, rtol=4e-4)
+
+
+@pytest.mark.parametrize("d,window", [(128, 0), (128, 200), (64, 77)])
+def test_output_independent_of_scoring_and_deterministic(d, window):
+    q, k, v = _qkv(b=2, hq=8, hk=2, n=1500, d=d, seed=d + window)
+    out1, imp1 = prefill(q, k, v, recency_decay=0.1, observation_window=window)
+    out2, imp2 = prefill(q, k, v, recency_decay=0.1, observation_window=window)
+    plain, none = prefill(q, k, v, score=False)
+    h2o = prefill(q, k, v, value_weighted=False)[0]
+    assert none is None
+    assert torch.equal(out1, out2) and torch.equal(out1, plain) and torch.equal(out1, h2o)
+    torch.testing.assert_close(imp1, imp2, rtol=1e-6, atol=0)    # atomics may reorder FP32 sums
+
+
+def test_kernel_resources():
+    res = flash_evict.kernel_resources()
+    names = {r["kernel"] for r in res}
+    assert "fused_fast<bf16,128,1>" in names and "select_rows" in names
+    fast = [r for r in res if r["kernel"] == "fused_fast<bf16,128,1>"][0]
+    assert 0 < fast["registers_per_thread"] <= 512 and fast["lds_dynamic_bytes"] > 0
