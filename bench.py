@@ -57,21 +57,36 @@ def algorithmic_flop(b, hq, n, d, window, causal=True):
     return 4 * d * p_attn + 2 * d * p_replay
 
 
-def cpu_baseline(q, k, v, kw, threads):
-    """Time the CPU oracle on one query head (all N queries) and extrapolate to the layer."""
+def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
+    """Time the CPU oracle on `sample_heads` query heads (all N queries, their KV heads) and
+    extrapolate to the layer; also time the library's host selection on the layer's scores."""
+    import ctypes
     import torch
     from oracle.attention import chunked
+    from flash_evict import _lib
     torch.set_num_threads(threads)
     b, hq, n, d = q.shape
-    qc, kc, vc = q[:1, :1].cpu(), k[:1, :1].cpu(), v[:1, :1].cpu()
+    hk = k.shape[1]
+    g = hq // hk
+    sample_heads = min(sample_heads, hq)
+    kv_needed = (sample_heads + g - 1) // g
+    qc, kc, vc = q[:1, :sample_heads].cpu(), k[:1, :kv_needed].cpu(), v[:1, :kv_needed].cpu()
     args = dict(causal=True, value_weighted=True, recency_decay=kw["recency_decay"],
                 observation_window=kw["observation_window"], block=1024)
     t0 = time.perf_counter()
-    chunked(qc, kc, vc, **args)
+    _, imp = chunked(qc, kc, vc, **args)
     dt = time.perf_counter() - t0
-    heads = b * hq
-    layer_s = dt * heads
+    layer_s = dt * (b * hq) / sample_heads
     flop = algorithmic_flop(b, hq, n, d, kw["observation_window"])
+    # host selection (fe_select_host) on a [B*Hkv, N] score array of the layer's size
+    scores = imp[0, :1].expand(b * hk, n).contiguous()
+    idx = torch.empty((b * hk, kw["budget"]), dtype=torch.int64)
+    mask = torch.empty((b * hk, n), dtype=torch.bool)
+    L = _lib.lib()
+    t1 = time.perf_counter()
+    _lib.check(L.fe_select_host(scores.data_ptr(), b * hk, n, n, kw["budget"], kw["reserved_recent"],
+                                kw["pool_kernel"], idx.data_ptr(), mask.data_ptr(), 0), "fe_select_host")
+    sel_ms = (time.perf_counter() - t1) * 1e3
     cpu_model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -82,14 +97,16 @@ def cpu_baseline(q, k, v, kw, threads):
     except OSError:
         pass
     return {
-        "value": flop / layer_s / 1e12,
+        "value": round(flop / layer_s / 1e12, 4),
         "unit": "TFLOP/s",
-        "ms_per_layer": layer_s * 1e3,
+        "ms_per_layer": round(layer_s * 1e3 + sel_ms, 1),
         "cores": threads,
         "kind": "port",
-        "sample": "oracle/attention.chunked (FP32 torch CPU, 1024-query blocks) on 1 of %d query heads "
-                  "(all %d queries, its KV head), %.2f s measured, x%d extrapolated; CPU %s"
-                  % (heads, n, dt, heads, cpu_model),
+        "select_host_ms": round(sel_ms, 2),
+        "sample": "oracle/attention.chunked (FP32 torch CPU, 1024-query blocks) on %d of %d query heads "
+                  "(all %d queries), %.2f s measured, x%g extrapolated; selection: fe_select_host on "
+                  "%d x %d scores (1 thread); CPU %s" % (sample_heads, b * hq, n, dt, (b * hq) / sample_heads,
+                                                          b * hk, n, cpu_model),
     }
 
 
@@ -100,7 +117,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "fused_traffic.json"),
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "fused_attn_score_headline_traffic.json"),
                     help="rocprofv3 PMC summary giving HBM bytes per fused launch (optional)")
     args = ap.parse_args()
 
