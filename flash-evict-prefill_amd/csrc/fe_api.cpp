@@ -95,6 +95,7 @@ extern "C" int fe_kernel_resources(char* buf, size_t cap) {
   std::string s = "[";
   append_attn_resources(s);
   append_select_resources(s);
+  append_gather_resources(s);
   if (s.size() > 1 && s.back() == ',') s.pop_back();
   s += "]";
   if (s == "[]") {

@@ -17,6 +17,7 @@ hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream);
 // Resource dump helpers: each kernel family appends JSON objects to `out`.
 void append_attn_resources(std::string& out);
 void append_select_resources(std::string& out);
+void append_gather_resources(std::string& out);
 
 // Fused-kernel timing (enabled through fe_fused_timing_enable).
 bool fused_timing_enabled();

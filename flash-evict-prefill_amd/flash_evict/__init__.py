@@ -7,6 +7,7 @@ runs in gfx950 HIP kernels behind the C ABI of libflash_evict_hip.so.
 import json
 
 from .prefill import prefill, evict, select_tokens
+from .cache import gather_tokens
 
 
 def kernel_resources():
@@ -22,4 +23,4 @@ def kernel_resources():
     return json.loads(buf.value.decode())
 
 
-__all__ = ["prefill", "evict", "select_tokens", "kernel_resources"]
+__all__ = ["prefill", "evict", "select_tokens", "gather_tokens", "kernel_resources"]

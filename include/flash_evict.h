@@ -14,6 +14,9 @@
  *                     sort, scatter_ of `select_tokens`), plus :180 (`~keep`) when invert=1
  *   fe_select_host    the same `select_tokens` body for CPU tensors (tests call it on CPU,
  *                     tests/test_prefill.py:77-84,149-159)
+ *   fe_gather_rows    kv_distill.cache.gather_tokens as called at
+ *                     flash_evict/kv_distill_adapter.py:38-39, streaming_adapter.py:86,
+ *                     quality_adapter.py:109-110 (KV compaction by the kept indices)
  *   fe_kernel_resources  scripts/benchmark.py:104-111 (`_prefill.device_caches` resource dump)
  */
 #ifndef FLASH_EVICT_H_
@@ -87,6 +90,19 @@ int fe_select(const float* scores, int64_t rows, int64_t n, int64_t row_stride,
 int fe_select_host(const float* scores, int64_t rows, int64_t n, int64_t row_stride,
                    int64_t budget, int64_t recent, int pool_kernel,
                    int64_t* indices_out, uint8_t* mask_out, int invert);
+
+/*
+ * KV compaction gather: out[b,h,j,:] = x[b,h,indices[b,h,j],:].
+ * x: [B,H,N,D] elements of elem_bytes (1, 2, 4 or 8) bytes with element strides
+ * x_strides = {b,h,n,d} (nonnegative); indices: [B,H,K] int64 with element strides
+ * index_strides = {b,h,j} (zero strides broadcast); out: contiguous [B,H,K,D].
+ * An index outside [0, N) yields a zero row. Rows move as 16-byte chunks when the
+ * channel stride is 1 and rows, strides and pointers are 16-byte aligned.
+ */
+int fe_gather_rows(const void* x, const int64_t* indices, void* out,
+                   int64_t B, int64_t H, int64_t N, int64_t D, int64_t K,
+                   const int64_t* x_strides, const int64_t* index_strides, int elem_bytes,
+                   void* hip_stream);
 
 /*
  * Timing of the fused attention+score kernel alone: when enabled, fe_prefill records a
