@@ -96,6 +96,7 @@ extern "C" int fe_kernel_resources(char* buf, size_t cap) {
   append_attn_resources(s);
   append_select_resources(s);
   append_gather_resources(s);
+  append_snap_resources(s);
   if (s.size() > 1 && s.back() == ',') s.pop_back();
   s += "]";
   if (s == "[]") {

@@ -18,6 +18,7 @@ hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream);
 void append_attn_resources(std::string& out);
 void append_select_resources(std::string& out);
 void append_gather_resources(std::string& out);
+void append_snap_resources(std::string& out);
 
 // Fused-kernel timing (enabled through fe_fused_timing_enable).
 bool fused_timing_enabled();

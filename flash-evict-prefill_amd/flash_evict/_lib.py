@@ -34,6 +34,9 @@ _SIGNATURES = {
                                       ctypes.c_int]),
     "fe_gather_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _I64P, _I64P, ctypes.c_int,
                                       _vp]),
+    "fe_snap_scores_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "fe_snap_scores": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _I64P, _I64P, ctypes.c_int,
+                                      _i64, _vp, ctypes.c_size_t, _vp]),
     "fe_fused_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "fe_fused_timing_read": (ctypes.c_int, [_I64P, ctypes.POINTER(ctypes.c_double)]),
     "fe_kernel_resources": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t]),

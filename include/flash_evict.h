@@ -17,6 +17,9 @@
  *   fe_gather_rows    kv_distill.cache.gather_tokens as called at
  *                     flash_evict/kv_distill_adapter.py:38-39, streaming_adapter.py:86,
  *                     quality_adapter.py:109-110 (KV compaction by the kept indices)
+ *   fe_snap_scores    flash_evict/baselines.py:15-27 (`snap_scores`, the SnapKV observation-
+ *                     window scores of the baseline path; its selection, snap_select at
+ *                     :30-40, is fe_select with recent = min(window, n, budget-1))
  *   fe_kernel_resources  scripts/benchmark.py:104-111 (`_prefill.device_caches` resource dump)
  */
 #ifndef FLASH_EVICT_H_
@@ -102,6 +105,22 @@ int fe_select_host(const float* scores, int64_t rows, int64_t n, int64_t row_str
 int fe_gather_rows(const void* x, const int64_t* indices, void* out,
                    int64_t B, int64_t H, int64_t N, int64_t D, int64_t K,
                    const int64_t* x_strides, const int64_t* index_strides, int elem_bytes,
+                   void* hip_stream);
+
+/*
+ * SnapKV observation-window scores (baseline path). With W = min(window, N) and
+ * G = Hq/Hkv, for every query head h of group j the last W query positions t give
+ *   p[h,t,:] = softmax_FP32(float(round_dtype(q[b,h,t,:] . k[b,j,n,:])) * D^-0.5,
+ *                           causal: n <= t)
+ *   scores[b,j,n] = (1/G) * sum_{h in group j} sum_t p[h,t,n]
+ * q: [B,Hq,N,D], k: [B,Hkv,N,D] with element strides {b,h,n,d}; scores: contiguous
+ * [B,Hkv,N] float32, every element written. workspace: device memory of at least
+ * fe_snap_scores_workspace_bytes(...) bytes. window >= 1.
+ */
+size_t fe_snap_scores_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t window);
+int fe_snap_scores(const void* q, const void* k, float* scores, int64_t B, int64_t Hq, int64_t Hkv,
+                   int64_t N, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                   int dtype, int64_t window, void* workspace, size_t workspace_bytes,
                    void* hip_stream);
 
 /*

@@ -14,6 +14,7 @@ Modules and the reference code each one restates (anishesg/flash-evict-prefill):
   select.snap_select       flash_evict/baselines.py:28-40
   select.avg_pool          torch avg_pool1d(k, stride 1, pad k//2, count_include_pad)
   brute                    pure-Python loops over the same definitions (tiny inputs only)
+  snap.snap_scores         flash_evict/baselines.py:15-27 (SnapKV observation-window scores)
   gather.gather_tokens     kv_distill.cache.gather_tokens as called at
                            flash_evict/kv_distill_adapter.py:38-39 (KV compaction)
   analytic                 closed forms used by tests/test_prefill.py:87-102,134-146
@@ -30,6 +31,9 @@ How each function is pinned (checked against something other than itself):
                 torch.sort / F.avg_pool1d on tie-free inputs, brute-force selection, and
                 the snap_select equivalence of tests/test_prefill.py:149-155.
   snap_select   torch.topk-based restatement on tie-free inputs.
+  snap_scores   the reference's own check (tests/test_baselines.py:19-20: a full window
+                gives the H2O mass of `materialized` / G), mass conservation (each key row
+                sums to W), the q = 0 closed form (uniform causal rows) and float64 loops.
   gather_tokens torch.gather on in-range indices, brute-force loops, and the call-site
                 identities (arange(N) gives the cache, the uniform_recent arange gives the
                 suffix slice, quality_adapter.py:41-43).
