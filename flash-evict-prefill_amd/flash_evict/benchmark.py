@@ -1,0 +1,163 @@
+"""Latency and PyTorch-allocator peak measurements of one attention layer.
+
+Same protocol as the reference's scripts/benchmark.py:18-126 (anishesg/flash-evict-prefill):
+per method two warm-up calls, `--repeats` calls timed with HIP events (median reported),
+then one more call with the allocator statistics reset around it; methods run in an
+order shuffled by a seeded RNG per sequence length; the report also lists the device
+kernels' registers, LDS and scratch (`kernel_resources`, standing in for the Triton
+`device_caches` dump at :104-111). Methods, for q [1,H,N,D], k/v [1,Hkv,N,D] bf16 and
+budget ceil(0.1 N):
+
+  torch_flash            torch's fused SDPA (the reference's baseline attention)
+  hip_attention_only     prefill(score=False)      (reference: triton_attention_only)
+  fused_replay_scores    prefill()
+  fused_replay_topk      evict(budget)
+  flash_snap_w32/_w128   flash_snap(budget, window)
+  gather_kv              gather_tokens of K and V by evict's kept indices (the adapters'
+                         compaction step; not a method of the reference script)
+
+Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
+--dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
+"""
+import argparse
+import gc
+import hashlib
+import json
+import math
+import os
+import random
+import statistics
+import subprocess
+from pathlib import Path
+
+import torch
+
+from . import evict, gather_tokens, kernel_resources, prefill
+from . import _lib
+from .baselines import flash_attention, flash_snap
+
+
+@torch.inference_mode()
+def measure(fn, repeats):
+    """Median of `repeats` event-timed calls after two warm-ups, then allocator peaks of
+    one more call (scripts/benchmark.py:18-49)."""
+    for _ in range(2):
+        result = fn()
+        del result
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        result = fn()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+        del result
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    before = torch.cuda.memory_stats()
+    free_before, total = torch.cuda.mem_get_info()
+    result = fn()
+    torch.cuda.synchronize()
+    after = torch.cuda.memory_stats()
+    record = {"median_ms": statistics.median(times), "samples_ms": times,
+              "allocated_before_bytes": before["allocated_bytes.all.current"],
+              "peak_allocated_bytes": after["allocated_bytes.all.peak"],
+              "peak_increment_bytes": after["allocated_bytes.all.peak"] - before["allocated_bytes.all.current"],
+              "peak_reserved_bytes": after["reserved_bytes.all.peak"],
+              "free_device_bytes_before": free_before, "total_device_bytes": total}
+    del result
+    return record
+
+
+def _tool_output(cmd):
+    """Text output of a diagnostic tool, or a note when it is unavailable."""
+    try:
+        return subprocess.run(cmd, capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError) as e:
+        return "unavailable: %s" % e
+
+
+def _git_revision():
+    try:
+        return subprocess.check_output(["git", "rev-parse", "HEAD"], text=True, stderr=subprocess.DEVNULL,
+                                       cwd=os.path.dirname(os.path.abspath(__file__))).strip()
+    except (OSError, subprocess.SubprocessError):
+        return None
+
+
+def _sources():
+    here = Path(__file__).resolve().parent
+    files = [here / "prefill.py", here / "baselines.py", here / "cache.py", Path(_lib.LIB_PATH)]
+    return {f.name: hashlib.sha256(f.read_bytes()).hexdigest() for f in files if f.exists()}
+
+
+def methods_for(q, k, v, budget):
+    """The timed callables of one sequence length."""
+    kept = {}
+
+    def gather_kv():
+        if "idx" not in kept:   # kept indices of one evict() call, made in the first warm-up
+            kept["idx"] = evict(q, k, v, budget)[2]
+        return gather_tokens(k, kept["idx"]), gather_tokens(v, kept["idx"])
+    return {
+        "torch_flash": lambda: flash_attention(q, k, v),
+        "hip_attention_only": lambda: prefill(q, k, v, score=False),
+        "fused_replay_scores": lambda: prefill(q, k, v),
+        "fused_replay_topk": lambda: evict(q, k, v, budget),
+        "flash_snap_w32": lambda: flash_snap(q, k, v, budget, 32),
+        "flash_snap_w128": lambda: flash_snap(q, k, v, budget, 128),
+        "gather_kv": gather_kv,
+    }
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser()
+    p.add_argument("--lengths", type=int, nargs="+", default=[8192, 32768, 131072])
+    p.add_argument("--heads", type=int, default=4)
+    p.add_argument("--kv-heads", type=int, default=2)
+    p.add_argument("--dim", type=int, default=64)
+    p.add_argument("--repeats", type=int, default=5)
+    p.add_argument("--methods", nargs="+", default=None, help="subset of the method names")
+    p.add_argument("--output", default="benchmark.json")
+    args = p.parse_args(argv)
+    torch.manual_seed(20260910)
+    output = Path(args.output)
+    output.parent.mkdir(parents=True, exist_ok=True)
+    report = {"args": vars(args), "gpu": torch.cuda.get_device_name(), "torch": torch.__version__,
+              "hip": torch.version.hip, "dtype": "bfloat16", "batch": 1, "git_revision": _git_revision(),
+              "source_sha256": _sources(), "rocm_smi_before": _tool_output(["rocm-smi"]),
+              "scope": "single attention layer; allocations include output and selection, exclude inputs",
+              "rows": []}
+    for n in args.lengths:
+        q = torch.randn((1, args.heads, n, args.dim), device="cuda", dtype=torch.bfloat16)
+        k = torch.randn((1, args.kv_heads, n, args.dim), device="cuda", dtype=q.dtype)
+        v = torch.randn_like(k)
+        budget = math.ceil(n * .1)
+        methods = methods_for(q, k, v, budget)
+        if args.methods:
+            methods = {name: fn for name, fn in methods.items() if name in args.methods}
+        # Seeded order reduces a systematic warm-up/temperature ordering effect.
+        items = list(methods.items())
+        random.Random(n).shuffle(items)
+        for name, fn in items:
+            try:
+                row = {"n": n, "method": name, "budget": budget, **measure(fn, args.repeats)}
+            except torch.OutOfMemoryError as e:
+                row = {"n": n, "method": name, "error": "OOM", "detail": str(e)}
+                gc.collect()
+                torch.cuda.empty_cache()
+            report["rows"].append(row)
+            report["kernel_resources"] = kernel_resources()
+            output.write_text(json.dumps(report, indent=2) + "\n")
+            print(json.dumps({key: val for key, val in row.items() if key != "samples_ms"}), flush=True)
+        del q, k, v
+        gc.collect()
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()
