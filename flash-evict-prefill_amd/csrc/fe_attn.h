@@ -17,6 +17,7 @@ struct AttnArgs {
   const u16* v;
   u16* out;
   float* imp;
+  float* bias;                      // split schedule: per-row replay bias out of traversal 1 (else null)
   long long qs[4], ks[4], vs[4];   // element strides {b, h, n, d}
   int N, D, G, Hq, Hkv, BH;
   int tiles_bh;                     // row tiles per (b, kv head): G * ceil(N/32)
@@ -57,6 +58,15 @@ struct FusedPlan {
 // Fast path (fe_attn_fast.hip): D in {64, 128}, positive scale, 16-byte rows, buffer-
 // addressable K/V. Returns false (and leaves `plan` untouched) when it does not apply.
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan);
+// Replay kernel of the split schedule (fe_attn_fast.hip): same layout rules as fast_plan;
+// launched with ReplayPlan::waves waves and ReplayPlan::rows row tiles per workgroup.
+struct ReplayPlan {
+  const void* fn;
+  int waves;
+  int rows;
+  const char* name;
+};
+bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan);
 hipError_t prepare_plan(const FusedPlan& plan);
 void append_fast_resources(std::string& out);
 

@@ -553,11 +553,17 @@ extern "C" int fe_zero_f32(float* p, int64_t n, void* hip_stream) {
   return FE_OK;
 }
 
-extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
-                          int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
-                          const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
-                          int value_weighted, int score, float recency_decay, int64_t window, void* hip_stream) {
-  clear_error();
+namespace fe {
+
+// Body of fe_prefill / fe_prefill_ws. With a workspace of fe_prefill_workspace_bytes()
+// bytes and the fast layouts, the replay runs as its own kernel (split schedule): the
+// attention kernel leaves each row's replay bias in the workspace, and replay_fast_kernel
+// runs the replay traversal at twice the occupancy. Otherwise one fused kernel does both.
+static int prefill_impl(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
+                        int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
+                        int value_weighted, int score, float recency_decay, int64_t window, void* workspace,
+                        size_t workspace_bytes, void* hip_stream) {
   if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || (score && !importance)) {
     set_error("fe_prefill: null pointer argument");
     return FE_ERR_INVALID;
@@ -599,6 +605,7 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
   a.v = (const u16*)v;
   a.out = (u16*)out;
   a.imp = importance;
+  a.bias = nullptr;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -626,6 +633,10 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
   a.ovec = (D % 4 == 0) && (((uintptr_t)out & 7u) == 0);
 
   FusedPlan plan;
+  ReplayPlan rplan;
+  const size_t ws_need = (size_t)(B * Hq * N) * sizeof(float);
+  const bool split = score && workspace && workspace_bytes >= ws_need && replay_plan(a, dtype, rplan);
+  if (split) a.bias = (float*)workspace;
   if (!fast_plan(a, dtype, plan)) {
     int dpi = 0;
     while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
@@ -664,6 +675,20 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;
   }
+  if (split) {
+    // Workgroups of rplan.rows row tiles; only those holding window rows are launched
+    // (tiles before query block win_lo/32 have none), heaviest first.
+    AttnArgs r = a;
+    r.wg_bh = (int)((tiles_bh + rplan.rows - 1) / rplan.rows);
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / rplan.rows;
+    const int64_t rgrid = B * Hkv * ((int64_t)r.wg_bh - wg_lo);
+    void* rargs[] = {&r};
+    err = hipLaunchKernel(rplan.fn, dim3((unsigned)rgrid), dim3(64 * rplan.waves), rargs, 0, stream);
+    if (err != hipSuccess) {
+      set_error(std::string("fe_prefill: replay kernel launch: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+  }
   if (timed) {
     if (hipEventRecord(ev1, stream) != hipSuccess) {
       set_error("fe_prefill: timing event record failed");
@@ -689,4 +714,30 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
     }
   }
   return FE_OK;
+}
+
+}  // namespace fe
+
+extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
+                          const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
+                          int value_weighted, int score, float recency_decay, int64_t window, void* hip_stream) {
+  clear_error();
+  return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
+                      causal, value_weighted, score, recency_decay, window, nullptr, 0, hip_stream);
+}
+
+extern "C" size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score) {
+  if (!score || B < 1 || Hq < 1 || N < 1) return 0;
+  return (size_t)(B * Hq * N) * sizeof(float);
+}
+
+extern "C" int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
+                             int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
+                             const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
+                             int value_weighted, int score, float recency_decay, int64_t window, void* workspace,
+                             size_t workspace_bytes, void* hip_stream) {
+  clear_error();
+  return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
+                      causal, value_weighted, score, recency_decay, window, workspace, workspace_bytes, hip_stream);
 }

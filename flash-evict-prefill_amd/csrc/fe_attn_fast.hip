@@ -320,7 +320,18 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
   }
 
   // ---------------- traversal 2: replay
-  if (!a.score || wg_q_hi - 1 < a.win_lo) return;
+  if (!a.score) return;
+  if (a.bias) {
+    // Split schedule: hand the row's replay bias (see below) to replay_fast_kernel.
+    const int qi = q0 + l32;
+    if (hh == 0 && tv && qi < N) {
+      const bool live = qi >= a.win_lo;
+      a.bias[(long long)(b * a.Hq + head) * N + qi] =
+          live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+    }
+    return;
+  }
+  if (wg_q_hi - 1 < a.win_lo) return;
 
   // p_qk * w_q / l_q = exp2(s*scale - b_q) with b_q = m_q + log2 l_q - decay*log2e*(q-N+1),
   // b_q = +inf for rows outside the window or past N. nb holds -b of the 16 rows of a lane.
@@ -413,7 +424,159 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
   flush((ntiles - 1) * BN, (ntiles - 1) & 1);
 }
 
+// Replay traversal of the split schedule. After fused_fast_kernel has written the bias
+//   b_q = m_q + log2 l_q - decay*log2e*(q - N + 1)   (+inf outside the window or past N)
+// of every query row, the importance is
+//   I[b, j, k] += sum over the group's heads and rows q of exp2(s_qk * scale*log2e - b_q)
+// (the value L1 norm is applied afterwards, as in the fused schedule). Without O, P and V
+// this traversal needs about half the registers and a third of the LDS of traversal 1, so
+// it runs at twice the occupancy (four waves per SIMD): eight waves of one row tile each
+// share every K tile, and each workgroup issues one FP32 atomic per key and tile.
+template <typename E, int DP>
+__global__ __launch_bounds__(512, 4) void replay_fast_kernel(const AttnArgs a) {
+  typedef FastTile<DP> T;
+  constexpr int BN = T::BN, NDC = T::NDC, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
+  constexpr int DPW = T::DMA_PER_WAVE;
+  constexpr int NW = 8;
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  constexpr float POS_INF = __builtin_huge_valf();
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[TILE], lds_k1[TILE];
+  __shared__ float red[2 * NW * BN];              // [2][NW][BN] per-wave column sums
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
+  const int N = a.N;
+
+  // heaviest causal query blocks first; the grid covers only workgroups with window rows
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
+  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
+  const int t_begin = wg * NW;
+  const int t_end = min(a.tiles_bh, t_begin + NW);
+  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
+  const int kv_end = a.causal ? wg_q_hi : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  const int t = t_begin + wv;
+  const bool tv = t < t_end;
+  const int tt = tv ? t : t_begin;
+  const int q0 = (tt / a.G) * 32;
+  const int head = hkv * a.G + (tt - (tt / a.G) * a.G);
+  const bool rin = tv && q0 + 31 >= a.win_lo;
+  const int wave_hi = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
+
+  // A operand: query row q0 + l32, channels 16c + 8h .. +7
+  u32x4 qf[NDC];
+  float nb[16];
+  {
+    const int qr = q0 + l32;
+    const bool ok = rin && qr < N;
+    const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+#pragma unroll
+    for (int c = 0; c < NDC; ++c) qf[c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
+    const float br = ok ? a.bias[(long long)(b * a.Hq + head) * N + qr] : POS_INF;
+    // the accumulator holds rows 8(i/4) + 4h + i%4 of the tile in register i
+#pragma unroll
+    for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+  }
+
+  // fixed per-lane K fragment offsets; the empty asm keeps them in registers (the compiler
+  // would otherwise recompute them in every tile, about 25 vector instructions)
+  u32 koff[NDC];
+#pragma unroll
+  for (int c = 0; c < NDC; ++c) {
+    koff[c] = (u32)(l32 * ROWB + (((2 * c + hh) ^ swz<DP>(l32)) << 4));
+    asm volatile("" : "+v"(koff[c]));
+  }
+  const u32 krow = (u32)(a.ks[2] * 2);
+  u32 dk[DPW];
+#pragma unroll
+  for (int r = 0; r < DPW; ++r) {
+    const int c = (r * 4 + (wv & 3)) * 64 + lane;
+    const int key = c / CPR, pc = c % CPR;
+    dk[r] = (u32)key * krow + (u32)(pc ^ swz<DP>(key)) * 16u;
+  }
+  const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+  float* imp_row = a.imp + (long long)bh * N;
+
+  auto flush = [&](int kb_prev, int buf_prev) {
+    if (tid < BN) {
+      const float* rr = red + buf_prev * NW * BN + tid;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
+      const int key = kb_prev + tid;
+      if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+    }
+  };
+
+  auto step = [&](int it, int BUF) __attribute__((always_inline)) {
+    const int kb = it * BN;
+    if (dmaw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it > 0) flush(kb - BN, BUF ^ 1);
+    if (dmaw && it + 1 < ntiles) dma_tile<DPW>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv);
+    float cs[2] = {0.f, 0.f};
+    if (kb <= wave_hi) {
+      const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        f32x16 sacc = (f32x16){};
+#pragma unroll
+        for (int c = 0; c < NDC; ++c)
+          sacc = E::mfma(qf[c], *(const u32x4*)(kt + koff[c] + s * 32 * ROWB), sacc);
+        // lanes hold key kb + 32s + l32; causal mask on diagonal tiles
+        if (a.causal && kb + BN - 1 > q0) {
+          const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[i];
+        }
+        float c4[4];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = fast_exp2(fmaf(sacc[i], a.scale_log2, nb[i]));
+          if (i < 4)
+            c4[i] = e;
+          else
+            c4[i & 3] += e;
+        }
+        cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+      }
+    }
+    cs[0] = half_swap_sum(cs[0]);
+    cs[1] = half_swap_sum(cs[1]);
+    if (hh == 0) {
+      float* rb = red + BUF * NW * BN + wv * BN;
+      rb[l32] = cs[0];
+      rb[32 + l32] = cs[1];
+    }
+  };
+
+  if (dmaw) dma_tile<DPW>(kg, krow, dk, 0, N, lds_k0, wv);
+  for (int it = 0; it < ntiles; it += 2) {
+    step(it, 0);
+    if (it + 1 < ntiles) step(it + 1, 1);
+  }
+  __syncthreads();
+  flush((ntiles - 1) * BN, (ntiles - 1) & 1);
+}
+
 namespace {
+
+template <typename E, int DP>
+ReplayPlan replay_entry(const char* name) {
+  return ReplayPlan{(const void*)replay_fast_kernel<E, DP>, 8, 8, name};
+}
+
+ReplayPlan g_replay[] = {
+    replay_entry<F16, 64>("replay_fast<f16,64>"),
+    replay_entry<F16, 128>("replay_fast<f16,128>"),
+    replay_entry<BF16, 64>("replay_fast<bf16,64>"),
+    replay_entry<BF16, 128>("replay_fast<bf16,128>"),
+};
 
 template <typename E, int DP>
 FusedPlan fast_entry(const char* name) {
@@ -446,7 +609,25 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   return true;
 }
 
+bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan) {
+  FusedPlan fp;
+  if (!fast_plan(a, dtype, fp)) return false;
+  plan = g_replay[(dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0)];
+  return true;
+}
+
 void append_fast_resources(std::string& out) {
+  for (const auto& e : g_replay) {
+    hipFuncAttributes attr;
+    if (hipFuncGetAttributes(&attr, e.fn) != hipSuccess) continue;
+    char buf[512];
+    snprintf(buf, sizeof(buf),
+             "{\"kernel\":\"%s\",\"registers_per_thread\":%d,\"lds_static_bytes\":%zu,"
+             "\"lds_dynamic_bytes\":0,\"scratch_bytes_per_thread\":%zu,\"max_threads_per_block\":%d},",
+             e.name, attr.numRegs, (size_t)attr.sharedSizeBytes, (size_t)attr.localSizeBytes,
+             attr.maxThreadsPerBlock);
+    out += buf;
+  }
   for (const auto& e : g_fast) {
     hipFuncAttributes attr;
     if (hipFuncGetAttributes(&attr, e.fn) != hipSuccess) continue;

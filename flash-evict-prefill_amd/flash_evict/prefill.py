@@ -73,12 +73,16 @@ def prefill(q, k, v, *, causal=True, value_weighted=True, score=True,
     L = _lib.lib()
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = L.fe_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                          importance.data_ptr() if score else None,
-                          b, h, hk, n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v),
-                          _DTYPES[q.dtype], scale, int(bool(causal)), int(bool(value_weighted)),
-                          int(bool(score)), recency_decay, window, stream)
-    _lib.check(rc, "fe_prefill")
+        # workspace of the split attention/replay schedule: one float per query row
+        ws_bytes = L.fe_prefill_workspace_bytes(b, h, n, int(bool(score)))
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device) if ws_bytes else None
+        rc = L.fe_prefill_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                             importance.data_ptr() if score else None,
+                             b, h, hk, n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v),
+                             _DTYPES[q.dtype], scale, int(bool(causal)), int(bool(value_weighted)),
+                             int(bool(score)), recency_decay, window,
+                             ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    _lib.check(rc, "fe_prefill_ws")
     return out, importance
 
 

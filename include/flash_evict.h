@@ -9,6 +9,8 @@
  * Reference interfaces replaced (paths are in anishesg/flash-evict-prefill):
  *   fe_prefill        flash_evict/prefill.py:128-136  (importance zero-init + the Triton
  *                     `_prefill[(cdiv(N,BM), B*Hq)](...)` launch, kernel at :14-83)
+ *   fe_prefill_ws     the same launch (prefill.py:128-136); the workspace carries the
+ *                     per-row replay bias between the attention and replay kernels
  *   fe_zero_f32       flash_evict/prefill.py:129      (`torch.zeros` of the score array)
  *   fe_select         flash_evict/prefill.py:160-169  (avg_pool1d, topk, tail arange/cat,
  *                     sort, scatter_ of `select_tokens`), plus :180 (`~keep`) when invert=1
@@ -66,6 +68,22 @@ int fe_prefill(const void* q, const void* k, const void* v, void* out, float* im
                const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
                int dtype, float scale, int causal, int value_weighted, int score,
                float recency_decay, int64_t window, void* hip_stream);
+
+/*
+ * fe_prefill with a caller-provided workspace (same contract and results up to FP32
+ * atomic order). With at least fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
+ * score != 0, else 0) and the fast layouts (D in {64,128}, positive scale, 16-byte rows),
+ * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
+ * per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace. With less
+ * workspace (or NULL) this is fe_prefill. Same reference interface as fe_prefill.
+ */
+size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score);
+int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance,
+                  int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                  int dtype, float scale, int causal, int value_weighted, int score,
+                  float recency_decay, int64_t window, void* workspace, size_t workspace_bytes,
+                  void* hip_stream);
 
 /* Zero-fill n floats with a fill kernel (graph-capture safe: no hipMemset node). */
 int fe_zero_f32(float* p, int64_t n, void* hip_stream);

@@ -1,0 +1,83 @@
+"""The two schedules of fe_prefill on the fast layouts agree: the fused single kernel
+(fe_prefill, no workspace) and the split attention + replay kernels (fe_prefill_ws, the
+path flash_evict.prefill takes). The attention output is bitwise identical (the replay does
+not touch it); the importance differs only by the order of FP32 atomic additions
+(rtol 2e-6, atol 1e-6 of the largest score). Both are checked against the oracle elsewhere
+through prefill(); this pins the workspace-free entry point to the same results."""
+import pytest
+import torch
+
+from flash_evict import _lib
+from flash_evict.prefill import _DTYPES
+
+from _helpers import seeded_randn, transposed_qkv
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, causal, weighted, decay, window, use_ws):
+    b, h, n, d = q.shape
+    hk = k.shape[1]
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    imp = torch.empty((b, hk, n), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    w = min(n, window or n)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), b, h, hk, n, d,
+            _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], d ** -0.5, int(causal),
+            int(weighted), 1, decay, w)
+    if use_ws:
+        nbytes = L.fe_prefill_workspace_bytes(b, h, n, 1)
+        assert nbytes == b * h * n * 4
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        rc = L.fe_prefill_ws(*args, ws.data_ptr(), nbytes, stream)
+    else:
+        rc = L.fe_prefill(*args, stream)
+    _lib.check(rc, "prefill")
+    torch.cuda.synchronize()
+    return out, imp
+
+
+CASES = [
+    # b, hq, hk, n, d, dtype, causal, weighted, decay, window, layout
+    (1, 32, 8, 4096, 128, torch.bfloat16, True, True, 0.1, 0, "transposed"),
+    (2, 8, 2, 1000, 64, torch.float16, True, False, 0.0, 0, "contiguous"),
+    (1, 28, 4, 3000, 128, torch.bfloat16, True, True, 0.0, 128, "contiguous"),
+    (1, 4, 4, 777, 128, torch.bfloat16, False, True, 0.05, 300, "transposed"),
+    (1, 8, 1, 65, 64, torch.float16, True, True, 0.0, 1, "contiguous"),
+]
+
+
+@pytest.mark.parametrize("b,hq,hk,n,d,dtype,causal,weighted,decay,window,layout", CASES)
+def test_split_and_fused_schedules_agree(b, hq, hk, n, d, dtype, causal, weighted, decay, window, layout):
+    print(f"schedules b={b} hq={hq} hk={hk} n={n} d={d} {dtype} causal={causal} window={window}", flush=True)
+    if layout == "transposed":
+        q, k, v = transposed_qkv(b, n, hq, hk, d, dtype, n + d)
+    else:
+        q = seeded_randn((b, hq, n, d), dtype, n)
+        k = seeded_randn((b, hk, n, d), dtype, n + 1)
+        v = seeded_randn((b, hk, n, d), dtype, n + 2)
+    o1, i1 = _run(q, k, v, causal, weighted, decay, window, use_ws=False)
+    o2, i2 = _run(q, k, v, causal, weighted, decay, window, use_ws=True)
+    assert torch.equal(o1, o2)
+    tol = 1e-6 * float(i1.abs().max())
+    assert float((i1 - i2).abs().max()) <= tol + 2e-6 * float(i1.abs().max())
+
+
+def test_small_workspace_falls_back_to_fused():
+    q = seeded_randn((1, 8, 512, 128), torch.bfloat16, 1)
+    k = seeded_randn((1, 2, 512, 128), torch.bfloat16, 2)
+    v = seeded_randn((1, 2, 512, 128), torch.bfloat16, 3)
+    o1, i1 = _run(q, k, v, True, True, 0.0, 0, use_ws=False)
+    L = _lib.lib()
+    out = torch.empty_like(q)
+    imp = torch.empty((1, 2, 512), dtype=torch.float32, device="cuda")
+    ws = torch.empty(16, dtype=torch.float32, device="cuda")
+    rc = L.fe_prefill_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), 1, 8, 2, 512,
+                         128, _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], 128 ** -0.5, 1, 1,
+                         1, 0.0, 512, ws.data_ptr(), 64, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "fe_prefill_ws")
+    torch.cuda.synchronize()
+    assert torch.equal(out, o1)
+    # same fused kernel; only the FP32 atomic order can differ between the two runs
+    assert float((imp - i1).abs().max()) <= 2e-6 * float(i1.abs().max())
