@@ -51,7 +51,8 @@ __device__ __forceinline__ u32x4 load8(const u16* row, long long sd, int d0, int
 struct FusedPlan {
   const void* fn;
   size_t lds;
-  int tpw;            // row tiles (32 queries of one head) per wave
+  int waves;          // waves per workgroup
+  int rows;           // row tiles (32 queries of one head) per workgroup
   const char* name;
 };
 

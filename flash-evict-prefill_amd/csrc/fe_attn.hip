@@ -591,8 +591,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   const int64_t G = Hq / Hkv;
   const int64_t nqs = (N + 31) / 32;
   const int64_t tiles_bh = G * nqs;
-  const int tpw = 1;
-  const int64_t wg_bh = (tiles_bh + 4 * tpw - 1) / (4 * tpw);
+  const int64_t wg_bh = (tiles_bh + 3) / 4;   // the most workgroups any plan uses
   const int64_t blocks = B * Hkv * wg_bh;
   if (N > (1LL << 30) || tiles_bh > (1LL << 30) || blocks > 0x7fffffffLL || B * Hkv > (1LL << 30)) {
     set_error("fe_prefill: problem too large for one launch");
@@ -641,10 +640,10 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     int dpi = 0;
     while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
     const FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
-    plan = FusedPlan{(const void*)ent.fn, ent.lds, 1, ent.name};
+    plan = FusedPlan{(const void*)ent.fn, ent.lds, 4, 4, ent.name};
   }
-  // Workgroups are sized by the plan's row tiles per wave.
-  a.wg_bh = (int)((tiles_bh + 4 * plan.tpw - 1) / (4 * plan.tpw));
+  // Workgroups are sized by the plan's row tiles per workgroup.
+  a.wg_bh = (int)((tiles_bh + plan.rows - 1) / plan.rows);
   const int64_t grid = B * Hkv * (int64_t)a.wg_bh;
 
   hipStream_t stream = (hipStream_t)hip_stream;
@@ -670,7 +669,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     }
   }
   void* kargs[] = {&a};
-  err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(256), kargs, plan.lds, stream);
+  err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
   if (err != hipSuccess) {
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;

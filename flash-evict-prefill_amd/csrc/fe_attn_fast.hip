@@ -54,7 +54,8 @@ struct FastTile {
   static constexpr int DMA_PER_WAVE = (BN * CPR) / 256;
   static constexpr int NDC = DP / 16;            // MFMA k-chunks of QK^T
   static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
-  static constexpr size_t LDS = 4 * (size_t)TILE + 2 * 4 * BN * 4;   // static LDS per workgroup
+  static constexpr int NW = 8;                   // waves (row tiles) per workgroup
+  static constexpr size_t LDS = 4 * (size_t)TILE + 2 * NW * BN * 4;  // static LDS per workgroup
 };
 
 // XOR applied to the 16-byte chunk index of row `key`. Two read patterns must be bank-
@@ -96,10 +97,10 @@ __device__ __forceinline__ void dma_tile(const unsigned char* g, u32 rowb, const
 }
 
 template <typename E, int DP>
-__global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
-  constexpr int DPW = T::DMA_PER_WAVE;
+  constexpr int DPW = T::DMA_PER_WAVE, NW = T::NW;
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -107,18 +108,19 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
   // one buffer) and the fragment reads of the other buffer do not alias, and the objects'
   // addresses are link-time constants that fold into the reads' offset fields.
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[TILE], lds_k1[TILE], lds_v0[TILE], lds_v1[TILE];
-  __shared__ float red[2 * 4 * BN];              // [2][4][BN] per-wave column sums
+  __shared__ float red[2 * NW * BN];             // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
   const int bh = (int)(blockIdx.x % (unsigned)a.BH);
   const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
   const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
-  const int t_begin = wg * 4;
-  const int t_end = min(a.tiles_bh, t_begin + 4);
+  const int t_begin = wg * NW;
+  const int t_end = min(a.tiles_bh, t_begin + NW);
   const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
   const int kv_end = a.causal ? wg_q_hi : N;
   const int ntiles = (kv_end + BN - 1) / BN;
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
   u32 dk[DPW], dv[DPW];
 #pragma unroll
   for (int r = 0; r < DPW; ++r) {
-    const int c = (r * 4 + wv) * 64 + lane;
+    const int c = (r * 4 + (wv & 3)) * 64 + lane;
     const int key = c / CPR, pc = c % CPR;
     const u32 lc = (u32)(pc ^ swz<DP>(key));
     dk[r] = (u32)key * krow + lc * 16u;
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
     const int kb = it * BN;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (it + 1 < ntiles) {
+    if (dmaw && it + 1 < ntiles) {
       dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
       dma(vg, vrow, dv, kb + BN, BUF == 0 ? lds_v1 : lds_v0);
     }
@@ -280,20 +282,27 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
     }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
+    // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
+    u32x4 vf[2][4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, c4, 0);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      u32x4 vf[4];
+      if (dt + 1 < NDT) {
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) vf[c4] = v_frag(BUF, c4, dt);
+        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, c4, dt + 1);
+      }
       FE_PRIO_HI();
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[c4], pb[c4], o[dt]);
+      for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[dt & 1][c4], pb[c4], o[dt]);
       FE_PRIO_LO();
     }
   };
 
-  dma(kg, krow, dk, 0, lds_k0);
-  dma(vg, vrow, dv, 0, lds_v0);
+  if (dmaw) {
+    dma(kg, krow, dk, 0, lds_k0);
+    dma(vg, vrow, dv, 0, lds_v0);
+  }
   for (int it = 0; it < ntiles; it += 2) {
     t1_step(it, 0);
     if (it + 1 < ntiles) t1_step(it + 1, 1);
@@ -347,12 +356,14 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
   const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
   float* imp_row = a.imp + (long long)bh * N;
 
-  // Flush of the previous tile's four per-wave column sums (written before the barrier
-  // that precedes this call): one atomic per key per workgroup.
+  // Flush of the previous tile's per-wave column sums (written before the barrier that
+  // precedes this call): one atomic per key per workgroup.
   auto flush = [&](int kb_prev, int buf_prev) {
     if (tid < BN) {
-      const float* rr = red + buf_prev * 4 * BN;
-      const float sum = (rr[tid] + rr[BN + tid]) + (rr[2 * BN + tid] + rr[3 * BN + tid]);
+      const float* rr = red + buf_prev * NW * BN + tid;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
       const int key = kb_prev + tid;
       if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
     }
@@ -365,7 +376,7 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (it > 0) flush(kb - BN, BUF ^ 1);
-    if (it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
+    if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
     float cs[2] = {0.f, 0.f};
     if (kb <= wave_hi_r) {
       f32x16 sacc[2];
@@ -407,7 +418,7 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
     cs[0] = half_swap_sum(cs[0]);
     cs[1] = half_swap_sum(cs[1]);
     if (hh == 0) {
-      float* rb = red + BUF * 4 * BN + wv * BN;
+      float* rb = red + BUF * NW * BN + wv * BN;
       rb[l32] = cs[0];
       rb[32 + l32] = cs[1];
     }
@@ -415,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void fused_fast_kernel(const AttnArgs a) {
 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave is done reading the traversal-1 tiles
-  dma(kg, krow, dk, 0, lds_k0);
+  if (dmaw) dma(kg, krow, dk, 0, lds_k0);
   for (int it = 0; it < ntiles; it += 2) {
     t2_step(it, 0);
     if (it + 1 < ntiles) t2_step(it + 1, 1);
@@ -580,7 +591,7 @@ ReplayPlan g_replay[] = {
 
 template <typename E, int DP>
 FusedPlan fast_entry(const char* name) {
-  return FusedPlan{(const void*)fused_fast_kernel<E, DP>, 0, 1, name};   // static LDS only
+  return FusedPlan{(const void*)fused_fast_kernel<E, DP>, 0, FastTile<DP>::NW, FastTile<DP>::NW, name};   // static LDS only
 }
 
 FusedPlan g_fast[] = {

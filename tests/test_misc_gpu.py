@@ -116,4 +116,4 @@ def test_kernel_resources():
     assert "fused_fast<bf16,128>" in names and "select_rows" in names
     fast = [r for r in res if r["kernel"] == "fused_fast<bf16,128>"][0]
     # K/V double buffers (4 x 64 rows x 256 B) plus the column-sum exchange, all static LDS
-    assert 0 < fast["registers_per_thread"] <= 256 and fast["lds_static_bytes"] == 4 * 64 * 256 + 2 * 4 * 64 * 4
+    assert 0 < fast["registers_per_thread"] <= 256 and fast["lds_static_bytes"] == 4 * 64 * 256 + 2 * 8 * 64 * 4
