@@ -440,15 +440,18 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
 // of every query row, the importance is
 //   I[b, j, k] += sum over the group's heads and rows q of exp2(s_qk * scale*log2e - b_q)
 // (the value L1 norm is applied afterwards, as in the fused schedule). Without O, P and V
-// this traversal needs about half the registers and a third of the LDS of traversal 1, so
-// it runs at twice the occupancy (four waves per SIMD): eight waves of one row tile each
-// share every K tile, and each workgroup issues one FP32 atomic per key and tile.
-template <typename E, int DP>
-__global__ __launch_bounds__(512, 4) void replay_fast_kernel(const AttnArgs a) {
+// this traversal needs far fewer registers than traversal 1. A workgroup holds 8 row tiles
+// that share every K tile (one FP32 atomic per key and tile per workgroup), as 8/TPW waves
+// of TPW row tiles each. TPW = 1 runs at four waves per SIMD; TPW = 2 (the default) at two,
+// with every K fragment read from LDS feeding two MFMAs: that halves the LDS read traffic,
+// the co-bottleneck of this traversal next to the MFMAs, and measures about 3% faster. (At
+// three waves per SIMD, TPW = 2 does not fit the 168-register budget without spills.)
+template <typename E, int DP, int TPW>
+__global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
   constexpr int DPW = T::DMA_PER_WAVE;
-  constexpr int NW = 8;
+  constexpr int NW = 8 / TPW;                    // waves per workgroup
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -465,33 +468,36 @@ __global__ __launch_bounds__(512, 4) void replay_fast_kernel(const AttnArgs a) {
   const int bh = (int)(blockIdx.x % (unsigned)a.BH);
   const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
   const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
-  const int t_begin = wg * NW;
-  const int t_end = min(a.tiles_bh, t_begin + NW);
+  const int t_begin = wg * 8;
+  const int t_end = min(a.tiles_bh, t_begin + 8);
   const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
   const int kv_end = a.causal ? wg_q_hi : N;
   const int ntiles = (kv_end + BN - 1) / BN;
 
-  const int t = t_begin + wv;
-  const bool tv = t < t_end;
-  const int tt = tv ? t : t_begin;
-  const int q0 = (tt / a.G) * 32;
-  const int head = hkv * a.G + (tt - (tt / a.G) * a.G);
-  const bool rin = tv && q0 + 31 >= a.win_lo;
-  const int wave_hi = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
-
-  // A operand: query row q0 + l32, channels 16c + 8h .. +7
-  u32x4 qf[NDC];
-  float nb[16];
-  {
-    const int qr = q0 + l32;
+  // This wave's row tiles j: 32 query positions from q0[j] of query head head[j]. A operand:
+  // query row q0 + l32, channels 16c + 8h .. +7; nb: minus the bias of the 16 rows a lane
+  // holds in the accumulator (register i: row 8(i/4) + 4h + i%4).
+  int q0[TPW];
+  u32x4 qf[TPW][NDC];
+  float nb[TPW][16];
+  int wave_hi = -1;
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = t_begin + TPW * wv + j;
+    const bool tv = t < t_end;
+    const int tt = tv ? t : t_begin;
+    q0[j] = (tt / a.G) * 32;
+    const int head = hkv * a.G + (tt - (tt / a.G) * a.G);
+    const bool rin = tv && q0[j] + 31 >= a.win_lo;
+    if (rin) wave_hi = max(wave_hi, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
+    const int qr = q0[j] + l32;
     const bool ok = rin && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
     const float br = ok ? a.bias[(long long)(b * a.Hq + head) * N + qr] : POS_INF;
-    // the accumulator holds rows 8(i/4) + 4h + i%4 of the tile in register i
 #pragma unroll
-    for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+    for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
   }
 
   // fixed per-lane K fragment offsets; the empty asm keeps them in registers (the compiler
@@ -535,24 +541,32 @@ __global__ __launch_bounds__(512, 4) void replay_fast_kernel(const AttnArgs a) {
       const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        f32x16 sacc = (f32x16){};
+        f32x16 sacc[TPW];
 #pragma unroll
-        for (int c = 0; c < NDC; ++c)
-          sacc = E::mfma(qf[c], *(const u32x4*)(kt + koff[c] + s * 32 * ROWB), sacc);
-        // lanes hold key kb + 32s + l32; causal mask on diagonal tiles
-        if (a.causal && kb + BN - 1 > q0) {
-          const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+        for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sacc[i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[i];
+        for (int c = 0; c < NDC; ++c) {
+          const u32x4 kf = *(const u32x4*)(kt + koff[c] + s * 32 * ROWB);
+#pragma unroll
+          for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
         }
         float c4[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(fmaf(sacc[i], a.scale_log2, nb[i]));
-          if (i < 4)
-            c4[i] = e;
-          else
-            c4[i & 3] += e;
+        for (int j = 0; j < TPW; ++j) {
+          // lanes hold key kb + 32s + l32; causal mask on diagonal tiles
+          if (a.causal && kb + BN - 1 > q0[j]) {
+            const int rel = kb + 32 * s + l32 - q0[j] - 4 * hh;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[j][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[j][i];
+          }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float e = fast_exp2(fmaf(sacc[j][i], a.scale_log2, nb[j][i]));
+            if (j == 0 && i < 4)
+              c4[i] = e;
+            else
+              c4[i & 3] += e;
+          }
         }
         cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
       }
@@ -577,9 +591,12 @@ __global__ __launch_bounds__(512, 4) void replay_fast_kernel(const AttnArgs a) {
 
 namespace {
 
+#ifndef FE_REPLAY_TPW
+#define FE_REPLAY_TPW 2
+#endif
 template <typename E, int DP>
 ReplayPlan replay_entry(const char* name) {
-  return ReplayPlan{(const void*)replay_fast_kernel<E, DP>, 8, 8, name};
+  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, FE_REPLAY_TPW>, 8 / FE_REPLAY_TPW, 8, name};
 }
 
 ReplayPlan g_replay[] = {
