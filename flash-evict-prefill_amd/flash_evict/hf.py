@@ -1,0 +1,168 @@
+"""Hugging Face transformers integration: fused prefill with importance inside a model, then
+KV-cache compaction by the kept indices.
+
+This stands in for the reference's kv_distill adapters (flash_evict/kv_distill_adapter.py:16-67,
+streaming_adapter.py:16-87, quality_adapter.py:38-52 of anishesg/flash-evict-prefill). Those
+patch the attention forwards of an older transformers release and drive kv_distill's
+Controller, a research package the reference does not vendor. Here the same flow uses the
+pluggable attention of current transformers (`AttentionInterface`): during a prefill
+forward every attention layer runs `prefill` (gfx950 kernels) and records its importance;
+`compress` then selects and gathers each layer's K/V (`select_tokens`, `gather_tokens`) into a
+new `DynamicCache`, and decoding continues from that cache at the original positions (the
+kept keys keep their RoPE rotation), as the reference's fused controller does after
+prefill. Decode steps (one query against the cache) use torch's SDPA, as the reference
+hands decoding to the upstream attention.
+"""
+import math
+
+import torch
+
+from .baselines import flash_attention, snap_scores, snap_select
+from .cache import gather_tokens
+from .prefill import prefill, select_tokens
+
+# registered attention implementation name (transformers treats names containing "flash" as
+# flash-attention kernels from its hub, so the name avoids that word)
+ATTN_NAME = "evict_prefill"
+_registered = False
+
+
+def _sdpa(module, query, key, value, attention_mask, **kwargs):
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    return sdpa_attention_forward(module, query, key, value, attention_mask, **kwargs)
+
+
+def _attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """The registered attention function: prefill (query length = key length) runs the fused
+    kernels and records the layer's state; anything else goes to SDPA."""
+    ctl = getattr(module, "_flash_evict_controller", None)
+    if ctl is None or ctl.mode != "prefill" or query.shape[2] != key.shape[2]:
+        return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
+    if query.shape[0] != 1:
+        raise ValueError("flash_evict prefill expects one unpadded prompt at a time")
+    layer = module.layer_idx
+    if ctl.backend == "fused":
+        out, importance = prefill(query, key, value, scale=scaling, **ctl.scoring)
+        ctl.states[layer] = {"k": key, "v": value, "importance": importance}
+    elif ctl.backend == "snap":
+        out = flash_attention(query, key, value)
+        ctl.states[layer] = {"k": key, "v": value, "snap": snap_scores(query, key, ctl.snap_window)}
+    else:   # "full"
+        out = flash_attention(query, key, value)
+        ctl.states[layer] = {"k": key, "v": value}
+    return out.transpose(1, 2), None
+
+
+def _register():
+    global _registered
+    if not _registered:
+        from transformers import AttentionInterface
+        from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+        AttentionInterface.register(ATTN_NAME, _attention)
+        AttentionMaskInterface.register(ATTN_NAME, sdpa_mask)
+        _registered = True
+
+
+def _budget(method_suffix, prompt_length):
+    """Budget of a method suffix as the reference's compress parses it
+    (kv_distill_adapter.py:31-33): 'full', a fraction ('0.1') or a count ('48')."""
+    if method_suffix == "full":
+        budget = prompt_length
+    elif "." in method_suffix:
+        budget = math.ceil(prompt_length * float(method_suffix))
+    else:
+        budget = int(method_suffix)
+    return max(1, min(budget, prompt_length))
+
+
+class EvictionController:
+    """Runs a model's prefill through the fused kernels and compacts its KV cache.
+
+    backend: "fused" (importance from the fused replay), "snap" (SnapKV scores of the last
+    `snap_window` queries, torch SDPA attention) or "full" (no scoring; compaction keeps
+    everything). `scoring` holds prefill keyword arguments (recency_decay,
+    observation_window, value_weighted). Use `mode = "prefill"` (the default after
+    construction) for the prompt forward, then `compress`.
+    """
+
+    def __init__(self, model, *, backend="fused", scoring=None, reserved_recent=0, pool_kernel=1, snap_window=32):
+        if backend not in ("fused", "snap", "full"):
+            raise ValueError("Unsupported backend")
+        _register()
+        self.model = model
+        self.backend = backend
+        self.scoring = dict(scoring or {})
+        self.reserved_recent = reserved_recent
+        self.pool_kernel = pool_kernel
+        self.snap_window = snap_window
+        self.states = {}
+        self.mode = "prefill"
+        self._previous = model.config._attn_implementation
+        self._modules = [m for m in model.modules() if hasattr(m, "layer_idx") and hasattr(m, "q_proj")]
+        for m in self._modules:
+            m._flash_evict_controller = self
+        model.set_attn_implementation(ATTN_NAME)
+
+    def reset(self):
+        self.states = {}
+        self.mode = "prefill"
+
+    def kept_indices(self, budget):
+        """Per layer, the ascending kept indices [B, Hkv, budget] of the method."""
+        kept = {}
+        for layer, state in self.states.items():
+            n = state["k"].shape[2]
+            b = max(1, min(budget, n))
+            if self.backend == "fused":
+                kept[layer] = select_tokens(state["importance"], b, recent=min(self.reserved_recent, b),
+                                            pool_kernel=self.pool_kernel)[0]
+            elif self.backend == "snap":
+                kept[layer] = snap_select(state["snap"], b, self.snap_window)[0]
+            else:
+                kept[layer] = torch.arange(n, device=state["k"].device).expand(*state["k"].shape[:2], n)
+        return kept
+
+    def compress(self, budget):
+        """Compact every layer's K/V to `budget` tokens (an int, or a method suffix such as
+        'fused_0.1' / '0.1' / '48' / 'full' as the reference's compress accepts) and return
+        the compacted `DynamicCache`. Switches to decode mode."""
+        from transformers import DynamicCache
+        if not self.states:
+            raise RuntimeError("compress needs a prefill forward first")
+        n = next(iter(self.states.values()))["k"].shape[2]
+        if isinstance(budget, str):
+            budget = _budget(budget.split("_")[-1], n)
+        kept = self.kept_indices(budget)
+        cache = DynamicCache()
+        for layer in sorted(self.states):
+            state = self.states[layer]
+            k = gather_tokens(state["k"], kept[layer])
+            v = gather_tokens(state["v"], kept[layer])
+            cache.update(k, v, layer)
+            self.states[layer] = {"k": k, "v": v}
+        self.mode = "decode"
+        return cache
+
+    def close(self):
+        """Restore the model's previous attention implementation."""
+        for m in self._modules:
+            if getattr(m, "_flash_evict_controller", None) is self:
+                del m._flash_evict_controller
+        self.model.set_attn_implementation(self._previous)
+
+
+def choose_indices(method, k, v, importance=None, snap=None):
+    """Kept indices of one evaluation policy (reference quality_adapter.py:38-52): None for
+    the full cache, a suffix for 'uniform_recent', the largest value L1 norms for
+    'value_norm_only', SnapKV for 'snap', and the fused importance otherwise."""
+    n = k.shape[2]
+    budget = min(n, method["budget"] or n)
+    if method["backend"] == "full" or budget == n:
+        return None
+    if method["backend"] == "uniform_recent":
+        return torch.arange(n - budget, n, device=k.device).expand(*k.shape[:2], budget)
+    if method["backend"] == "value_norm_only":
+        return select_tokens(v.float().abs().sum(-1), budget)[0]
+    if method["backend"] == "snap":
+        return snap_select(snap, budget, window=32, kernel=5)[0]
+    return select_tokens(importance, budget, reserved_recent=min(budget, method["reserved_recent"]))[0]
