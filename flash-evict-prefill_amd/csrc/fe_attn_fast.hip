@@ -107,7 +107,9 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   // One LDS object per buffer: the waitcount pass can then tell that a tile's DMA (into
   // one buffer) and the fragment reads of the other buffer do not alias, and the objects'
   // addresses are link-time constants that fold into the reads' offset fields.
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[TILE], lds_k1[TILE], lds_v0[TILE], lds_v1[TILE];
+  // Two buffers per operand, each holding two consecutive 64-key tiles (slots 0 and 1).
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[2 * TILE], lds_k1[2 * TILE], lds_v0[2 * TILE],
+      lds_v1[2 * TILE];
   __shared__ float red[2 * NW * BN];             // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
@@ -184,15 +186,16 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     dma_tile<DPW>(g, rowb, doff, kb, N, ldst, wv);
   };
 
-  // K fragments of keys 32*s + l32 from buffer BUF
-  auto k_frags = [&](int BUF, int s, u32x4(&kf)[NDC]) __attribute__((always_inline)) {
-    const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
+  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT
+  auto k_frags = [&](int BUF, int SLOT, int s, u32x4(&kf)[NDC]) __attribute__((always_inline)) {
+    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
 #pragma unroll
     for (int c = 0; c < NDC; ++c) kf[c] = *(const u32x4*)(kt + koff[c] + s * 32 * ROWB);
   };
-  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF (two transposing reads)
-  auto v_frag = [&](int BUF, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
-    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + 16 * c4 * ROWB;
+  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT (two transposing
+  // reads)
+  auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
+    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + 16 * c4 * ROWB;
     const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[0][dt]));
     const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[1][dt]));
     const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
@@ -205,24 +208,32 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
 
   // ---------------- traversal 1
+  // Tiles are processed in pairs per barrier: buffer BUF holds tiles it and it+1 while the
+  // DMA fills the other buffer with tiles it+2 and it+3.
+  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (dmaw) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+        if (it + 2 + sl < ntiles) {
+          dma(kg, krow, dk, (it + 2 + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+          dma(vg, vrow, dv, (it + 2 + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+        }
+    }
+  };
   // One 64-key tile: S^T = K Q^T (two 32-key accumulators; lanes hold queries), mask on
   // diagonal and ragged tiles, exact running max with O/l rescale only when some row's max
   // rose, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
-  auto t1_step = [&](int it, int BUF) __attribute__((always_inline)) {
+  auto t1_step = [&](int it, int BUF, int SLOT) __attribute__((always_inline)) {
     const int kb = it * BN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (dmaw && it + 1 < ntiles) {
-      dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
-      dma(vg, vrow, dv, kb + BN, BUF == 0 ? lds_v1 : lds_v0);
-    }
     if (kb > wave_hi) return;
 
     f32x16 sacc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       u32x4 kf[NDC];
-      k_frags(BUF, s, kf);
+      k_frags(BUF, SLOT, s, kf);
       FE_PRIO_HI();
       sacc[s] = E::mfma(kf[0], qf[0], (f32x16){});
 #pragma unroll
@@ -285,12 +296,12 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
     u32x4 vf[2][4];
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, c4, 0);
+    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       if (dt + 1 < NDT) {
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, c4, dt + 1);
+        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
       }
       FE_PRIO_HI();
 #pragma unroll
@@ -300,12 +311,22 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   };
 
   if (dmaw) {
-    dma(kg, krow, dk, 0, lds_k0);
-    dma(vg, vrow, dv, 0, lds_v0);
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+      if (sl < ntiles) {
+        dma(kg, krow, dk, sl * BN, lds_k0 + sl * TILE);
+        dma(vg, vrow, dv, sl * BN, lds_v0 + sl * TILE);
+      }
   }
-  for (int it = 0; it < ntiles; it += 2) {
-    t1_step(it, 0);
-    if (it + 1 < ntiles) t1_step(it + 1, 1);
+  for (int it = 0; it < ntiles; it += 4) {
+    t1_sync(it, 0);
+    t1_step(it, 0, 0);
+    if (it + 1 < ntiles) t1_step(it + 1, 0, 1);
+    if (it + 2 < ntiles) {
+      t1_sync(it + 2, 1);
+      t1_step(it + 2, 1, 0);
+      if (it + 3 < ntiles) t1_step(it + 3, 1, 1);
+    }
   }
 
   // ---------------- finish rows
@@ -383,7 +404,7 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         u32x4 kf[NDC];
-        k_frags(BUF, s, kf);
+        k_frags(BUF, 0, s, kf);
         FE_PRIO_HI();
         sacc[s] = E::mfma(qf[0], kf[0], (f32x16){});
 #pragma unroll

@@ -115,5 +115,6 @@ def test_kernel_resources():
     names = {r["kernel"] for r in res}
     assert "fused_fast<bf16,128>" in names and "select_rows" in names
     fast = [r for r in res if r["kernel"] == "fused_fast<bf16,128>"][0]
-    # K/V double buffers (4 x 64 rows x 256 B) plus the column-sum exchange, all static LDS
-    assert 0 < fast["registers_per_thread"] <= 256 and fast["lds_static_bytes"] == 4 * 64 * 256 + 2 * 8 * 64 * 4
+    # K/V double buffers of two 64-key tiles (8 x 64 rows x 256 B) plus the column-sum
+    # exchange of the eight waves, all static LDS
+    assert 0 < fast["registers_per_thread"] <= 256 and fast["lds_static_bytes"] == 8 * 64 * 256 + 2 * 8 * 64 * 4
