@@ -15,7 +15,8 @@
 // the threshold key T of the (budget-recent)-th largest score with LDS histograms; one
 // ordered pass then keeps key > T plus the first ties at T, and a block prefix sum gives
 // each kept token its output slot, so indices come out ascending and the mask is written
-// in the same pass. One 256-thread workgroup per row.
+// in the same pass. One 1024-thread workgroup per row; the passes over a row read 16-byte
+// vectors when the row is 16-byte aligned.
 #include <math.h>
 #include <string>
 
@@ -32,7 +33,10 @@ __device__ __forceinline__ u32 order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive prefix sum over the 256 threads of a block; `total` receives the block sum.
+constexpr int kSelThreads = 1024;               // threads of a selection workgroup (one row)
+constexpr int kSelWaves = kSelThreads / 64;
+
+// Exclusive prefix sum over the threads of a selection workgroup; `total` receives the sum.
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int x = v;
@@ -46,7 +50,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total)
   int before = 0;
   total = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kSelWaves; ++i) {
     const int t = tmp[i];
     before += (i < w) ? t : 0;
     total += t;
@@ -71,17 +75,19 @@ __global__ __launch_bounds__(256) void avg_pool_kernel(const float* s, long long
   out[row * (long long)m + i] = acc / (float)k;
 }
 
-__global__ __launch_bounds__(256) void select_rows_kernel(const float* src, long long src_stride, int m, int K,
-                                                          int n, int recent, long long* idx, int budget,
-                                                          unsigned char* mask, int invert) {
+__global__ __launch_bounds__(kSelThreads) void select_rows_kernel(const float* src, long long src_stride, int m,
+                                                                  int K, int n, int recent, long long* idx,
+                                                                  int budget, unsigned char* mask, int invert) {
+  constexpr int ST = kSelThreads;
   __shared__ u32 hist[2048];
-  __shared__ int scan_tmp[4];
+  __shared__ int scan_tmp[kSelWaves];
   __shared__ u32 sh_prefix;
   __shared__ int sh_kk;
   __shared__ u32 sh_eq;
   const int tid = threadIdx.x;
   const long long row = blockIdx.x;
   const float* x = src + row * src_stride;
+  const bool vec = ((uintptr_t)x & 15u) == 0;   // 16-byte loads of 4 scores
   long long* irow = idx ? idx + row * (long long)budget : nullptr;
   unsigned char* mrow = mask ? mask + row * (long long)n : nullptr;
   const unsigned char keep_v = invert ? 0 : 1, drop_v = invert ? 1 : 0;
@@ -94,15 +100,26 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const float* src, long
       const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
       const int bits = pass == 2 ? 10 : 11;
       const int nb = 1 << bits;
-      for (int i = tid; i < nb; i += 256) hist[i] = 0u;
+      for (int i = tid; i < nb; i += ST) hist[i] = 0u;
       __syncthreads();
-      for (int i = tid; i < m; i += 256) {
-        const u32 key = order_key(x[i]);
+      auto count = [&](float f) __attribute__((always_inline)) {
+        const u32 key = order_key(f);
         if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & (u32)(nb - 1)], 1u);
+      };
+      for (int i = 4 * tid; i < m; i += 4 * ST) {
+        if (vec && i + 3 < m) {
+          const float4 v = *(const float4*)(x + i);
+          count(v.x);
+          count(v.y);
+          count(v.z);
+          count(v.w);
+        } else {
+          for (int e = 0; e < 4 && i + e < m; ++e) count(x[i + e]);
+        }
       }
       __syncthreads();
       // Thread t owns bins [nb - (t+1)*bpt, nb - t*bpt): thread 0 holds the highest digits.
-      const int bpt = nb / 256;
+      const int bpt = nb / ST;
       const int hi_bin = nb - 1 - tid * bpt;
       int local = 0;
       for (int e = 0; e < bpt; ++e) local += (int)hist[hi_bin - e];
@@ -129,15 +146,24 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const float* src, long
     const int need_eq = kk;     // ties at T still to keep, lowest index first
     const bool all_eq = (int)eq_total == need_eq;
     int out_base = 0, eq_base = 0;
-    for (int c0 = 0; c0 < m; c0 += 256 * 8) {
+    for (int c0 = 0; c0 < m; c0 += ST * 8) {
       const int i0 = c0 + tid * 8;
+      float xv[8];
+      if (vec && i0 + 7 < m) {
+        const float4 a0 = *(const float4*)(x + i0), a1 = *(const float4*)(x + i0 + 4);
+        xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+        xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = i0 + e < m ? x[i0 + e] : 0.f;
+      }
       bool gt[8], eq[8];
       int neq = 0;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = i0 + e;
         const bool valid = i < m;
-        const u32 key = valid ? order_key(x[i]) : 0u;
+        const u32 key = valid ? order_key(xv[e]) : 0u;
         gt[e] = valid && key > T;
         eq[e] = valid && key == T;
         neq += eq[e] ? 1 : 0;
@@ -168,9 +194,9 @@ __global__ __launch_bounds__(256) void select_rows_kernel(const float* src, long
       }
     }
   } else if (mrow) {
-    for (int i = tid; i < m; i += 256) mrow[i] = drop_v;
+    for (int i = tid; i < m; i += ST) mrow[i] = drop_v;
   }
-  for (int j = tid; j < recent; j += 256) {
+  for (int j = tid; j < recent; j += ST) {
     if (irow) irow[K + j] = (long long)(m + j);
     if (mrow) mrow[m + j] = keep_v;
   }
@@ -278,7 +304,8 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
     src = (const float*)workspace;
     src_stride = m;
   }
-  hipLaunchKernelGGL(select_rows_kernel, dim3((unsigned)rows), dim3(256), 0, stream, src, src_stride, m, K, (int)n,
+  hipLaunchKernelGGL(select_rows_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, src, src_stride, m, K,
+                     (int)n,
                      (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out, invert ? 1 : 0);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {

@@ -18,6 +18,10 @@ budget ceil(0.1 N):
 
 Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
 --dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
+
+`--kernels` instead times the HBM-bound kernels on scaled synthetics (the headline's score
+array is only 1 MiB, where they are launch-latency bound) and reports achieved GB/s against
+algorithmic bytes (each input byte read once, each output byte written once).
 """
 import argparse
 import gc
@@ -114,6 +118,58 @@ def methods_for(q, k, v, budget):
     }
 
 
+def _event_ms(fn, repeats):
+    """Median HIP-event time of `fn` (on torch's current stream) after two warm-ups."""
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    return statistics.median(times)
+
+
+@torch.inference_mode()
+def kernel_rows(repeats):
+    """Scaled-synthetic timings of the zero-fill, selection and gather kernels."""
+    from .prefill import _select
+    rows, n, budget, recent = 256, 131072, 1024, 64
+    g = torch.Generator(device="cuda").manual_seed(20260910)
+    scores = torch.rand((rows, n), device="cuda", generator=g)
+    out = []
+
+    def row(name, fn, nbytes, shape):
+        ms = _event_ms(fn, repeats)
+        out.append({"kernel": name, "shape": shape, "median_ms": ms, "algorithmic_bytes": nbytes,
+                    "GB/s": nbytes / (ms * 1e-3) / 1e9, "frac_of_8TB/s": nbytes / (ms * 1e-3) / 8e12})
+        print(json.dumps(out[-1]), flush=True)
+
+    zbuf = torch.empty(rows * n, dtype=torch.float32, device="cuda")
+    L = _lib.lib()
+
+    def zero():
+        _lib.check(L.fe_zero_f32(zbuf.data_ptr(), zbuf.numel(), torch.cuda.current_stream().cuda_stream), "fe_zero_f32")
+    row("zero_f32", zero, rows * n * 4, "%d x %d float32" % (rows, n))
+    sel_bytes = rows * n * 4 + rows * n + rows * budget * 8
+    row("select (top-k + mask + indices)", lambda: _select(scores, budget, recent, 1, False), sel_bytes,
+        "%d rows x %d, budget %d, recent %d" % (rows, n, budget, recent))
+    pool_bytes = sel_bytes + 2 * rows * (n - recent) * 4
+    row("select with pool 5", lambda: _select(scores, budget, recent, 5, False), pool_bytes,
+        "%d rows x %d, budget %d, recent %d, pool 5 (pooled scores written and read once)" % (rows, n, budget, recent))
+    h, keys, d, keep = 8, 131072, 128, 65536
+    cache = torch.randn((1, keys, h, d), device="cuda", generator=g).to(torch.bfloat16).transpose(1, 2)
+    idx = torch.sort(torch.randperm(keys, device="cuda", generator=g)[:keep]).values.expand(1, h, keep).contiguous()
+    gbytes = 2 * h * keep * d * 2 + h * keep * 8
+    row("gather_tokens", lambda: gather_tokens(cache, idx), gbytes,
+        "%d heads x %d of %d rows x %d bf16 (transposed view)" % (h, keep, keys, d))
+    return out
+
+
 def main(argv=None):
     p = argparse.ArgumentParser()
     p.add_argument("--lengths", type=int, nargs="+", default=[8192, 32768, 131072])
@@ -123,7 +179,13 @@ def main(argv=None):
     p.add_argument("--repeats", type=int, default=5)
     p.add_argument("--methods", nargs="+", default=None, help="subset of the method names")
     p.add_argument("--output", default="benchmark.json")
+    p.add_argument("--kernels", action="store_true", help="time the HBM-bound kernels on scaled synthetics")
     args = p.parse_args(argv)
+    if args.kernels:
+        report = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "hip": torch.version.hip,
+                  "rows": kernel_rows(args.repeats)}
+        Path(args.output).write_text(json.dumps(report, indent=2) + "\n")
+        return
     torch.manual_seed(20260910)
     output = Path(args.output)
     output.parent.mkdir(parents=True, exist_ok=True)

@@ -28,3 +28,12 @@ def test_harness_runs_every_method(tmp_path):
         assert r["budget"] == (26 if r["n"] == 256 else 30)
     kernels = {e["kernel"] for e in report["kernel_resources"]}
     assert any(k.startswith("fused_fast") for k in kernels) and "gather_rows16_kernel" in kernels
+
+
+def test_kernel_mode(tmp_path):
+    out = tmp_path / "k.json"
+    benchmark.main(["--kernels", "--repeats", "2", "--output", str(out)])
+    rows = json.loads(out.read_text())["rows"]
+    assert [r["kernel"] for r in rows] == ["zero_f32", "select (top-k + mask + indices)", "select with pool 5",
+                                          "gather_tokens"]
+    assert all(r["median_ms"] > 0 and r["GB/s"] > 0 for r in rows)
