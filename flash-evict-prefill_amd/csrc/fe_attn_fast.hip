@@ -2,16 +2,19 @@
 // 16-byte K/V rows. Same mathematics as the generic kernel in fe_attn.hip (reference
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
 //
+//   * A workgroup is 8 waves of one 32-query row tile each, all on one KV head (GQA
+//     packing), so each K/V tile in LDS serves 8 row tiles; waves 0-3 issue the DMA.
+//   * The K/V buffers hold pairs of 64-key tiles: one barrier per 128 keys.
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
 //     (scalar arithmetic only), so rows past N read as zero and no VALU work is spent on
 //     addresses. LDS rows are stored unpadded with the 16-byte chunk index XOR-swizzled by
 //     the key, so fragment reads are bank-conflict free.
 //   * Every LDS read uses a per-lane offset register fixed for the whole kernel plus an
-//     immediate (key half, 16-key group, buffer): the buffers are separate LDS objects and
-//     the tile loop is unrolled by two, so no address arithmetic remains in the loop, and
-//     the waitcount pass can see that the DMA into one buffer does not alias reads of the
-//     other (reads of tile t never wait for the DMA of tile t+1).
+//     immediate (key half, 16-key group, buffer, slot): the buffers are separate LDS objects
+//     and the tile loop is unrolled over both buffers, so no address arithmetic remains in
+//     the loop, and the waitcount pass can see that the DMA into one buffer does not alias
+//     reads of the other (reads of tiles t, t+1 never wait for the DMA of t+2, t+3).
 //   * The A operand of O^T = V^T P^T (eight keys of one channel per lane) comes straight
 //     from the row-major V tile with two ds_read_b64_tr_b16 transposing reads; the key
 //     order of the read matches the S^T accumulator row order that becomes P^T.
@@ -55,7 +58,6 @@ struct FastTile {
   static constexpr int NDC = DP / 16;            // MFMA k-chunks of QK^T
   static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
   static constexpr int NW = 8;                   // waves (row tiles) per workgroup
-  static constexpr size_t LDS = 4 * (size_t)TILE + 2 * NW * BN * 4;  // static LDS per workgroup
 };
 
 // XOR applied to the 16-byte chunk index of row `key`. Two read patterns must be bank-
