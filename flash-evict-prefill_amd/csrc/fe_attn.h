@@ -27,6 +27,7 @@ struct AttnArgs {
   float decay_log2;                 // recency_decay * log2(e)
   int neg_scale;
   int causal, score, win_lo;        // win_lo = N - W
+  int rsplit;                       // replay kernel: key splits per workgroup of row tiles
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
 };
 

@@ -605,6 +605,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.out = (u16*)out;
   a.imp = importance;
   a.bias = nullptr;
+  a.rsplit = 1;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -680,7 +681,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     AttnArgs r = a;
     r.wg_bh = (int)((tiles_bh + rplan.rows - 1) / rplan.rows);
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / rplan.rows;
-    const int64_t rgrid = B * Hkv * ((int64_t)r.wg_bh - wg_lo);
+    const int64_t nwg = B * Hkv * ((int64_t)r.wg_bh - wg_lo);
+    // Split the keys of each workgroup when there are too few workgroups to fill the chip
+    // (short observation windows): about 1024 blocks, at least one key tile per split.
+    const int64_t max_tiles = (N + 63) / 64;
+    int64_t rs = (1024 + nwg - 1) / nwg;
+    rs = rs < 1 ? 1 : (rs > max_tiles ? max_tiles : rs);
+    r.rsplit = (int)rs;
+    const int64_t rgrid = nwg * rs;
     void* rargs[] = {&r};
     err = hipLaunchKernel(rplan.fn, dim3((unsigned)rgrid), dim3(64 * rplan.waves), rargs, 0, stream);
     if (err != hipSuccess) {

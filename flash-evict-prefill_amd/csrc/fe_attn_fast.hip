@@ -487,15 +487,23 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
-  // heaviest causal query blocks first; the grid covers only workgroups with window rows
-  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
-  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
+  // Heaviest causal query blocks first; the grid covers only workgroups with window rows.
+  // With few such workgroups (a short observation window) each one's keys are split over
+  // a.rsplit blocks (block-uniform: an empty share exits before any barrier).
+  const int ks = (int)(blockIdx.x % (unsigned)a.rsplit);
+  const int rest = (int)(blockIdx.x / (unsigned)a.rsplit);
+  const int bh = rest % a.BH;
+  const int wg = a.wg_bh - 1 - rest / a.BH;
   const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
   const int t_begin = wg * 8;
   const int t_end = min(a.tiles_bh, t_begin + 8);
   const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
   const int kv_end = a.causal ? wg_q_hi : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  const int ntiles_all = (kv_end + BN - 1) / BN;
+  const int per = (ntiles_all + a.rsplit - 1) / a.rsplit;
+  const int it_lo = ks * per;                     // this block's key tiles [it_lo, ntiles)
+  const int ntiles = min(ntiles_all, it_lo + per);
+  if (it_lo >= ntiles) return;
 
   // This wave's row tiles j: 32 query positions from q0[j] of query head head[j]. A operand:
   // query row q0 + l32, channels 16c + 8h .. +7; nb: minus the bias of the 16 rows a lane
@@ -557,7 +565,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
     const int kb = it * BN;
     if (dmaw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (it > 0) flush(kb - BN, BUF ^ 1);
+    if (it > it_lo) flush(kb - BN, BUF ^ 1);
     if (dmaw && it + 1 < ntiles) dma_tile<DPW>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv);
     float cs[2] = {0.f, 0.f};
     if (kb <= wave_hi) {
@@ -603,13 +611,13 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
     }
   };
 
-  if (dmaw) dma_tile<DPW>(kg, krow, dk, 0, N, lds_k0, wv);
-  for (int it = 0; it < ntiles; it += 2) {
+  if (dmaw) dma_tile<DPW>(kg, krow, dk, it_lo * BN, N, lds_k0, wv);
+  for (int it = it_lo; it < ntiles; it += 2) {
     step(it, 0);
     if (it + 1 < ntiles) step(it + 1, 1);
   }
   __syncthreads();
-  flush((ntiles - 1) * BN, (ntiles - 1) & 1);
+  flush((ntiles - 1) * BN, (ntiles - 1 - it_lo) & 1);
 }
 
 namespace {
