@@ -13,7 +13,11 @@ Prints one JSON line on stdout:
   cpu_baseline = the CPU oracle (oracle/attention.chunked) on one query head of the same
                  workload, extrapolated to the layer (reported only)
 Algorithmic work: 4*D*P_attn + 2*D*P_replay with P_attn = B*Hq*N(N+1)/2 (causal) and
-P_replay the (window-restricted) count of replayed query-key pairs.
+P_replay the count of query-key pairs the replay must visit: those of the last R query rows,
+R = fe_replay_rows(N, window, recency_decay). R is the observation window less the oldest
+rows whose recency weight exp(-decay*(N-1-q)) is exactly zero in FP32 (decay*(N-1-q) >= 105);
+they add exactly nothing to the importance and are not replayed (the reference replays
+them anyway). `config.nominal_tflop` gives the count over the whole window for comparison.
 """
 import argparse
 import json
@@ -45,8 +49,17 @@ def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
 
 
-def algorithmic_flop(b, hq, n, d, window, causal=True):
-    w = min(n, window or n)
+def replay_rows(n, window, recency_decay):
+    """Query rows the library's replay visits (fe_replay_rows)."""
+    from flash_evict import _lib
+    rows = _lib.lib().fe_replay_rows(n, min(n, window or n), float(recency_decay))
+    if rows < 1:
+        raise ValueError("fe_replay_rows rejected n=%d window=%d decay=%g" % (n, window, recency_decay))
+    return rows
+
+
+def algorithmic_flop(b, hq, n, d, window, recency_decay=0.0, causal=True, effective=True):
+    w = replay_rows(n, window, recency_decay) if effective else min(n, window or n)
     if causal:
         p_attn = b * hq * n * (n + 1) // 2
         # sum_{q=n-w}^{n-1} (q+1)
@@ -77,7 +90,7 @@ def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
     _, imp = chunked(qc, kc, vc, **args)
     dt = time.perf_counter() - t0
     layer_s = dt * (b * hq) / sample_heads
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"])
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
     # host selection (fe_select_host) on a [B*Hkv, N] score array of the layer's size
     scores = imp[0, :1].expand(b * hk, n).contiguous()
     idx = torch.empty((b * hk, kw["budget"]), dtype=torch.int64)
@@ -168,7 +181,8 @@ def main():
                    "fe_fused_timing_read")
     ms = elapsed * 1e3 / args.steps
     log("timed %d steps: %.3f ms/layer" % (args.steps, ms))
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"])
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
+    nominal = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
     fused_avg_ms = fused_ms.value / max(1, launches.value)
     achieved = flop / (fused_avg_ms * 1e-3) / 1e12
     traffic = None
@@ -194,7 +208,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v resident in HBM)",
         "config": {"workload": "evict() layer, %s" % args.config, "B": b, "Hq": hq, "Hkv": hk, "N": n, "D": d,
-                   "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4)},
+                   "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4),
+                   "replay_rows": replay_rows(n, kw["observation_window"], kw["recency_decay"]),
+                   "nominal_tflop": round(nominal / 1e12, 4)},
         "roofline": {"bound": "mfma", "kernel": "fused_attn_score", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches.value},

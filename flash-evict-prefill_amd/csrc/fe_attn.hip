@@ -9,6 +9,7 @@
 //   * out = acc / l in the input dtype                                      (:59-60)
 //   * replay only where (query block end) > N - W                           (:61)
 //   * w_q = exp(decay*(q-(N-1))) for N-W <= q < N, else 0                   (:66-67)
+//     (rows whose w_q underflows to exactly 0 in FP32 are not replayed: replay_rows)
 //   * p = exp2(s - m_q) / l_q, column sums over queries and grouped heads   (:68-77)
 //   * x ||v_k||_1 when value weighted                                       (:78-81)
 //   * FP32 atomic accumulation into I[b, kvhead, k]                         (:82-83)
@@ -559,6 +560,19 @@ namespace fe {
 // bytes and the fast layouts, the replay runs as its own kernel (split schedule): the
 // attention kernel leaves each row's replay bias in the workspace, and replay_fast_kernel
 // runs the replay traversal at twice the occupancy. Otherwise one fused kernel does both.
+// Query rows the replay must visit: the last `window` rows, less those whose recency weight
+// is exactly zero in FP32. A row at distance t = N-1-q from the end has weight
+// exp(-decay*t) (reference flash_evict/prefill.py:66, reference.py:19), which is below
+// 2^-151 once decay*t >= 105 and rounds to 0 in FP32, so the row adds exactly nothing to any
+// column; the replay's own term exp2(s*scale*log2e - b_q) is bounded by
+// 2^(-decay*log2e*t) <= 2^-151.4 there and underflows to 0 as well. Rows with t < 105/decay
+// are kept: ceil(105/decay) of them, or all `window` rows when that is fewer.
+int64_t replay_rows(int64_t N, int64_t window, float recency_decay) {
+  if (!(recency_decay > 0.f)) return window;
+  const double span = ceil(105.0 / (double)recency_decay);
+  return span < (double)window ? (int64_t)span : window;
+}
+
 static int prefill_impl(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
                         const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
@@ -626,7 +640,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.decay_log2 = (float)((double)recency_decay * log2e);
   a.causal = causal ? 1 : 0;
   a.score = score ? 1 : 0;
-  a.win_lo = (int)(N - window);
+  a.win_lo = (int)(N - replay_rows(N, window, recency_decay));
   a.qvec = vec_ok(q, q_strides, D);
   a.kvec = vec_ok(k, k_strides, D);
   a.vvec = vec_ok(v, v_strides, D);
@@ -732,6 +746,11 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
   clear_error();
   return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
                       causal, value_weighted, score, recency_decay, window, nullptr, 0, hip_stream);
+}
+
+extern "C" int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay) {
+  if (N < 1 || window < 1 || window > N || !isfinite(recency_decay) || recency_decay < 0.f) return -1;
+  return replay_rows(N, window, recency_decay);
 }
 
 extern "C" size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score) {

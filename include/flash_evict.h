@@ -70,6 +70,17 @@ int fe_prefill(const void* q, const void* k, const void* v, void* out, float* im
                float recency_decay, int64_t window, void* hip_stream);
 
 /*
+ * Number of query rows the importance replay of fe_prefill visits: `window`, less the
+ * oldest rows whose recency weight exp(-recency_decay*(N-1-q)) is exactly zero in FP32
+ * (recency_decay*(N-1-q) >= 105), i.e. min(window, ceil(105/recency_decay)) when
+ * recency_decay > 0. Those rows contribute exactly zero to every column in the reference
+ * (flash_evict/prefill.py:66-67 weights them by an underflowed 0.0), so skipping them does
+ * not change the importance. -1 for arguments fe_prefill would reject. No counterpart in
+ * the reference (which replays every window row); for work accounting and tests.
+ */
+int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
+
+/*
  * fe_prefill with a caller-provided workspace (same contract and results up to FP32
  * atomic order). With at least fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
  * score != 0, else 0) and the fast layouts (D in {64,128}, positive scale, 16-byte rows),

@@ -97,7 +97,7 @@ def test_long_uniform_analytic(n):
 
 # tests/test_prefill.py:105-131
 @pytest.mark.parametrize("n,decay,window", [
-    (512, .01, 0), (1024, .1, 0), (4096, 1., 0),
+    (512, .01, 0), (1024, .1, 0), (4096, 1., 0), (4096, .1, 0),
     (137, 0., 32), (1024, 0., 64), (4096, 0., 128),
     (137, .1, 65), (65, 1., 128), (1, .1, 32),
 ])
