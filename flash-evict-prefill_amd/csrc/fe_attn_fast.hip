@@ -35,9 +35,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // Raise the wave's issue priority around MFMA blocks so that, of the two waves sharing a
 // SIMD, the one with matrix work ready issues it first while the other fills the MFMA
 // shadow with its softmax VALU work.
-#ifndef FE_LAG
-#define FE_LAG 0
-#endif
 #ifndef FE_SETPRIO
 #define FE_SETPRIO 1
 #endif
@@ -112,29 +109,9 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   // One LDS object per buffer: the waitcount pass can then tell that a tile's DMA (into
   // one buffer) and the fragment reads of the other buffer do not alias, and the objects'
   // addresses are link-time constants that fold into the reads' offset fields.
-#if FE_LAG
-  // A ring of four single-tile slots per operand (slot = tile & 3).
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[TILE], lds_k1[TILE], lds_k2[TILE], lds_k3[TILE],
-      lds_v0[TILE], lds_v1[TILE], lds_v2[TILE], lds_v3[TILE];
-  auto kslot = [&](int S) __attribute__((always_inline)) -> unsigned char* {
-    return S == 0 ? lds_k0 : S == 1 ? lds_k1 : S == 2 ? lds_k2 : lds_k3;
-  };
-  auto vslot = [&](int S) __attribute__((always_inline)) -> unsigned char* {
-    return S == 0 ? lds_v0 : S == 1 ? lds_v1 : S == 2 ? lds_v2 : lds_v3;
-  };
-  constexpr int T2S = 1;                          // traversal-2 buffer b -> slot b
-#else
-  // Two buffers per operand, each holding two consecutive 64-key tiles (slots 2*b, 2*b+1).
+  // Two buffers per operand, each holding two consecutive 64-key tiles (slots 0 and 1).
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[2 * TILE], lds_k1[2 * TILE], lds_v0[2 * TILE],
       lds_v1[2 * TILE];
-  auto kslot = [&](int S) __attribute__((always_inline)) -> unsigned char* {
-    return ((S >> 1) == 0 ? lds_k0 : lds_k1) + (S & 1) * TILE;
-  };
-  auto vslot = [&](int S) __attribute__((always_inline)) -> unsigned char* {
-    return ((S >> 1) == 0 ? lds_v0 : lds_v1) + (S & 1) * TILE;
-  };
-  constexpr int T2S = 2;                          // traversal-2 buffer b -> slot 2*b
-#endif
   __shared__ float red[2 * NW * BN];             // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
@@ -211,15 +188,16 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     dma_tile<DPW>(g, rowb, doff, kb, N, ldst, wv);
   };
 
-  // K fragments of keys 32*s + l32 from tile slot S
-  auto k_frags = [&](int S, int s, u32x4(&kf)[NDC]) __attribute__((always_inline)) {
-    const unsigned char* kt = kslot(S);
+  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT
+  auto k_frags = [&](int BUF, int SLOT, int s, u32x4(&kf)[NDC]) __attribute__((always_inline)) {
+    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
 #pragma unroll
     for (int c = 0; c < NDC; ++c) kf[c] = *(const u32x4*)(kt + koff[c] + s * 32 * ROWB);
   };
-  // V^T fragment of channel tile dt, 16-key group c4, tile slot S (two transposing reads)
-  auto v_frag = [&](int S, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
-    const unsigned char* vt = vslot(S) + 16 * c4 * ROWB;
+  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT (two transposing
+  // reads)
+  auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
+    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + 16 * c4 * ROWB;
     const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[0][dt]));
     const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[1][dt]));
     const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
@@ -232,23 +210,39 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
 
   // ---------------- traversal 1
-  // Phases of one 64-key tile. qk: S^T = K Q^T (two 32-key accumulators; lanes hold
-  // queries). soft: mask on diagonal and ragged tiles, exact running max with O/l rescale
-  // only when some row's max rose, P = exp2(S*scale - m) rounded to the input dtype.
-  // pv: O^T += V^T P^T.
-  auto qk = [&](int S, f32x16(&sacc)[2]) __attribute__((always_inline)) {
+  // Tiles are processed in pairs per barrier: buffer BUF holds tiles it and it+1 while the
+  // DMA fills the other buffer with tiles it+2 and it+3.
+  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (dmaw) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+        if (it + 2 + sl < ntiles) {
+          dma(kg, krow, dk, (it + 2 + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+          dma(vg, vrow, dv, (it + 2 + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+        }
+    }
+  };
+  // One 64-key tile: S^T = K Q^T (two 32-key accumulators; lanes hold queries), mask on
+  // diagonal and ragged tiles, exact running max with O/l rescale only when some row's max
+  // rose, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
+  auto t1_step = [&](int it, int BUF, int SLOT) __attribute__((always_inline)) {
+    const int kb = it * BN;
+    if (kb > wave_hi) return;
+
+    f32x16 sacc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       u32x4 kf[NDC];
-      k_frags(S, s, kf);
+      k_frags(BUF, SLOT, s, kf);
       FE_PRIO_HI();
       sacc[s] = E::mfma(kf[0], qf[0], (f32x16){});
 #pragma unroll
       for (int c = 1; c < NDC; ++c) sacc[s] = E::mfma(kf[c], qf[c], sacc[s]);
       FE_PRIO_LO();
     }
-  };
-  auto soft = [&](int kb, f32x16(&sacc)[2], u32x4(&pb)[4]) __attribute__((always_inline)) {
+
     if (kb + BN - 1 > lo_lim) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
@@ -281,6 +275,7 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     }
     const float nm = m_run == NEG_INF ? 0.f : -m_run;
 
+    u32x4 pb[4];
     float ps[4];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -299,17 +294,16 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
                                  E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
     }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-  };
-  auto pv = [&](int S, const u32x4(&pb)[4]) __attribute__((always_inline)) {
+
     // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
     u32x4 vf[2][4];
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(S, c4, 0);
+    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       if (dt + 1 < NDT) {
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(S, c4, dt + 1);
+        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
       }
       FE_PRIO_HI();
 #pragma unroll
@@ -318,126 +312,25 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     }
   };
 
-#if FE_LAG
-  // Waves w and w+4 share a SIMD. Waves 0-3 run each tile's phases in order (qk, soft, pv)
-  // between two barriers; waves 4-7 run behind them (soft and pv of the previous tile, then
-  // qk of this one), so the vector work of one wave of a SIMD meets the matrix work of the
-  // other instead of both contending for the same unit at once. The four-slot ring keeps
-  // the previous tile resident for the lagging waves: the DMA issued after barrier t fills
-  // slot (t+2)&3, whose tile t-2 every wave has finished reading before barrier t.
-  auto sync = [&](int it) __attribute__((always_inline)) {
-    if (dmaw) {
-      // tile `it` has landed; the DMA of tile it+1 (issued one barrier later) may not have
-      if (it + 1 < ntiles) {
-        if constexpr (DPW == 4)
-          asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-  auto issue = [&](int it, int S) __attribute__((always_inline)) {
-    if (dmaw && it < ntiles) {
-      dma(kg, krow, dk, it * BN, kslot(S));
-      dma(vg, vrow, dv, it * BN, vslot(S));
-    }
-  };
-  static_assert(2 * DPW == 8 || 2 * DPW == 4, "DMA loads per tile");
-  issue(0, 0);
-  issue(1, 1);
-  if (wv < 4) {
-    auto step = [&](int it, int S) __attribute__((always_inline)) {
-      sync(it);
-      issue(it + 2, (S + 2) & 3);
-      const int kb = it * BN;
-      if (kb <= wave_hi) {
-        f32x16 sacc[2];
-        u32x4 pb[4];
-        qk(S, sacc);
-        soft(kb, sacc, pb);
-        pv(S, pb);
-      }
-    };
-    for (int it = 0; it < ntiles; it += 4) {
-      step(it, 0);
-      if (it + 1 < ntiles) step(it + 1, 1);
-      if (it + 2 < ntiles) step(it + 2, 2);
-      if (it + 3 < ntiles) step(it + 3, 3);
-    }
-  } else {
-    f32x16 sacc[2];  // S^T of the previous tile, carried across the barrier
-    auto step = [&](int it, int S) __attribute__((always_inline)) {
-      sync(it);
-      const int kb = it * BN;
-      if (it > 0 && kb - BN <= wave_hi) {
-        u32x4 pb[4];
-        soft(kb - BN, sacc, pb);
-        pv((S + 3) & 3, pb);
-      }
-      if (kb <= wave_hi) qk(S, sacc);
-    };
-    for (int it = 0; it < ntiles; it += 4) {
-      step(it, 0);
-      if (it + 1 < ntiles) step(it + 1, 1);
-      if (it + 2 < ntiles) step(it + 2, 2);
-      if (it + 3 < ntiles) step(it + 3, 3);
-    }
-    const int kl = (ntiles - 1) * BN;
-    if (kl <= wave_hi) {
-      u32x4 pb[4];
-      soft(kl, sacc, pb);
-      pv((ntiles - 1) & 3, pb);
-    }
-  }
-#else
-  // Tiles are processed in pairs per barrier: slots 2*BUF and 2*BUF+1 hold tiles it and
-  // it+1 while the DMA fills the other buffer with tiles it+2 and it+3.
-  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (dmaw) {
-#pragma unroll
-      for (int sl = 0; sl < 2; ++sl)
-        if (it + 2 + sl < ntiles) {
-          dma(kg, krow, dk, (it + 2 + sl) * BN, kslot(2 * (BUF ^ 1) + sl));
-          dma(vg, vrow, dv, (it + 2 + sl) * BN, vslot(2 * (BUF ^ 1) + sl));
-        }
-    }
-  };
-  auto t1_step = [&](int it, int S) __attribute__((always_inline)) {
-    const int kb = it * BN;
-    if (kb > wave_hi) return;
-    f32x16 sacc[2];
-    u32x4 pb[4];
-    qk(S, sacc);
-    soft(kb, sacc, pb);
-    pv(S, pb);
-  };
-
   if (dmaw) {
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
       if (sl < ntiles) {
-        dma(kg, krow, dk, sl * BN, kslot(sl));
-        dma(vg, vrow, dv, sl * BN, vslot(sl));
+        dma(kg, krow, dk, sl * BN, lds_k0 + sl * TILE);
+        dma(vg, vrow, dv, sl * BN, lds_v0 + sl * TILE);
       }
   }
   for (int it = 0; it < ntiles; it += 4) {
     t1_sync(it, 0);
-    t1_step(it, 0);
-    if (it + 1 < ntiles) t1_step(it + 1, 1);
+    t1_step(it, 0, 0);
+    if (it + 1 < ntiles) t1_step(it + 1, 0, 1);
     if (it + 2 < ntiles) {
       t1_sync(it + 2, 1);
-      t1_step(it + 2, 2);
-      if (it + 3 < ntiles) t1_step(it + 3, 3);
+      t1_step(it + 2, 1, 0);
+      if (it + 3 < ntiles) t1_step(it + 3, 1, 1);
     }
   }
-#endif
+
   // ---------------- finish rows
   const float l_tot = half_swap_sum(l_run);
   {
@@ -506,14 +399,14 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (it > 0) flush(kb - BN, BUF ^ 1);
-    if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, kslot(T2S * (BUF ^ 1)));
+    if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
     float cs[2] = {0.f, 0.f};
     if (kb <= wave_hi_r) {
       f32x16 sacc[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         u32x4 kf[NDC];
-        k_frags(T2S * BUF, s, kf);
+        k_frags(BUF, 0, s, kf);
         FE_PRIO_HI();
         sacc[s] = E::mfma(qf[0], kf[0], (f32x16){});
 #pragma unroll
@@ -556,7 +449,7 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave is done reading the traversal-1 tiles
-  if (dmaw) dma(kg, krow, dk, 0, kslot(0));
+  if (dmaw) dma(kg, krow, dk, 0, lds_k0);
   for (int it = 0; it < ntiles; it += 2) {
     t2_step(it, 0);
     if (it + 1 < ntiles) t2_step(it + 1, 1);
