@@ -6,18 +6,19 @@ headline shape B=1, Hq=32, Hkv=8, N=32768, D=128, causal, budget 1024, recency_d
 reserved_recent 64, all-query replay (observation_window 0).
 
 Prints one JSON line on stdout:
-  value        = algorithmic attention+score TFLOP per layer / measured layer time
+  value        = the layer's algorithmic attention+score TFLOP / measured layer time
   ms_per_step  = ms per layer (the metric's first half)
-  roofline     = the fused kernel alone: algorithmic TFLOP / its mean duration, timed with
-                 HIP events recorded by the library on the kernel's own stream
+  roofline     = the fused kernel alone: the TFLOP it executes / its mean duration, timed
+                 with HIP events recorded by the library on the kernel's own stream
   cpu_baseline = the CPU oracle (oracle/attention.chunked) on one query head of the same
                  workload, extrapolated to the layer (reported only)
-Algorithmic work: 4*D*P_attn + 2*D*P_replay with P_attn = B*Hq*N(N+1)/2 (causal) and
-P_replay the count of query-key pairs the replay must visit: those of the last R query rows,
-R = fe_replay_rows(N, window, recency_decay). R is the observation window less the oldest
-rows whose recency weight exp(-decay*(N-1-q)) is exactly zero in FP32 (decay*(N-1-q) >= 105);
-they add exactly nothing to the importance and are not replayed (the reference replays
-them anyway). `config.nominal_tflop` gives the count over the whole window for comparison.
+Algorithmic work of a layer (the metric's definition): 4*D*P_attn + 2*D*P_replay with
+P_attn = B*Hq*N(N+1)/2 (causal) and P_replay the query-key pairs of the last W query rows
+(W = the observation window, all rows when 0). The library replays only the last
+R = fe_replay_rows(N, W, recency_decay) of them: rows whose recency weight
+exp(-decay*(N-1-q)) is exactly zero in FP32 (decay*(N-1-q) >= 105) add exactly nothing to the
+importance. The roofline counts the work executed (R rows), so its fraction of peak is the
+MFMA utilisation; `config` lists both counts.
 """
 import argparse
 import json
@@ -90,7 +91,7 @@ def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
     _, imp = chunked(qc, kc, vc, **args)
     dt = time.perf_counter() - t0
     layer_s = dt * (b * hq) / sample_heads
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
     # host selection (fe_select_host) on a [B*Hkv, N] score array of the layer's size
     scores = imp[0, :1].expand(b * hk, n).contiguous()
     idx = torch.empty((b * hk, kw["budget"]), dtype=torch.int64)
@@ -181,10 +182,10 @@ def main():
                    "fe_fused_timing_read")
     ms = elapsed * 1e3 / args.steps
     log("timed %d steps: %.3f ms/layer" % (args.steps, ms))
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
-    nominal = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
+    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
+    executed = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
     fused_avg_ms = fused_ms.value / max(1, launches.value)
-    achieved = flop / (fused_avg_ms * 1e-3) / 1e12
+    achieved = executed / (fused_avg_ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(args.traffic_json):
         try:
@@ -210,7 +211,7 @@ def main():
         "config": {"workload": "evict() layer, %s" % args.config, "B": b, "Hq": hq, "Hkv": hk, "N": n, "D": d,
                    "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4),
                    "replay_rows": replay_rows(n, kw["observation_window"], kw["recency_decay"]),
-                   "nominal_tflop": round(nominal / 1e12, 4)},
+                   "executed_tflop": round(executed / 1e12, 4)},
         "roofline": {"bound": "mfma", "kernel": "fused_attn_score", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches.value},
