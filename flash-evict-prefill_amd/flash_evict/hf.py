@@ -12,6 +12,11 @@ new `DynamicCache`, and decoding continues from that cache at the original posit
 kept keys keep their RoPE rotation), as the reference's fused controller does after
 prefill. Decode steps (one query against the cache) use torch's SDPA, as the reference
 hands decoding to the upstream attention.
+
+`StreamingController` compacts each layer's K/V as soon as that layer's prefill attention
+has run (reference streaming_adapter.py:16-87), so the full caches of all layers are never
+held together; `chunk_mlp` bounds the feed-forward activations of long prompts
+(streaming_adapter.py:30-51).
 """
 import math
 
@@ -43,13 +48,13 @@ def _attention(module, query, key, value, attention_mask, scaling=None, dropout=
     layer = module.layer_idx
     if ctl.backend == "fused":
         out, importance = prefill(query, key, value, scale=scaling, **ctl.scoring)
-        ctl.states[layer] = {"k": key, "v": value, "importance": importance}
+        ctl._store(layer, {"k": key, "v": value, "importance": importance})
     elif ctl.backend == "snap":
         out = flash_attention(query, key, value)
-        ctl.states[layer] = {"k": key, "v": value, "snap": snap_scores(query, key, ctl.snap_window)}
+        ctl._store(layer, {"k": key, "v": value, "snap": snap_scores(query, key, ctl.snap_window)})
     else:   # "full"
         out = flash_attention(query, key, value)
-        ctl.states[layer] = {"k": key, "v": value}
+        ctl._store(layer, {"k": key, "v": value})
     return out.transpose(1, 2), None
 
 
@@ -107,41 +112,54 @@ class EvictionController:
         self.states = {}
         self.mode = "prefill"
 
+    def _store(self, layer, state):
+        """Keep one layer's prefill state (K, V and its scores) until `compress`."""
+        self.states[layer] = state
+
+    def _indices(self, state, budget):
+        """Ascending kept indices [B, Hkv, budget] of one layer's state, or None to keep all."""
+        n = state["k"].shape[2]
+        b = max(1, min(budget, n))
+        if self.backend == "fused":
+            return select_tokens(state["importance"], b, recent=min(self.reserved_recent, b),
+                                 pool_kernel=self.pool_kernel)[0]
+        if self.backend == "snap":
+            return snap_select(state["snap"], b, self.snap_window)[0]
+        return None
+
     def kept_indices(self, budget):
         """Per layer, the ascending kept indices [B, Hkv, budget] of the method."""
         kept = {}
         for layer, state in self.states.items():
-            n = state["k"].shape[2]
-            b = max(1, min(budget, n))
-            if self.backend == "fused":
-                kept[layer] = select_tokens(state["importance"], b, recent=min(self.reserved_recent, b),
-                                            pool_kernel=self.pool_kernel)[0]
-            elif self.backend == "snap":
-                kept[layer] = snap_select(state["snap"], b, self.snap_window)[0]
-            else:
-                kept[layer] = torch.arange(n, device=state["k"].device).expand(*state["k"].shape[:2], n)
+            idx = self._indices(state, budget)
+            if idx is None:
+                n = state["k"].shape[2]
+                idx = torch.arange(n, device=state["k"].device).expand(*state["k"].shape[:2], n)
+            kept[layer] = idx
         return kept
+
+    def _cache(self):
+        from transformers import DynamicCache
+        cache = DynamicCache()
+        for layer in sorted(self.states):
+            cache.update(self.states[layer]["k"], self.states[layer]["v"], layer)
+        return cache
 
     def compress(self, budget):
         """Compact every layer's K/V to `budget` tokens (an int, or a method suffix such as
         'fused_0.1' / '0.1' / '48' / 'full' as the reference's compress accepts) and return
         the compacted `DynamicCache`. Switches to decode mode."""
-        from transformers import DynamicCache
         if not self.states:
             raise RuntimeError("compress needs a prefill forward first")
         n = next(iter(self.states.values()))["k"].shape[2]
         if isinstance(budget, str):
             budget = _budget(budget.split("_")[-1], n)
         kept = self.kept_indices(budget)
-        cache = DynamicCache()
         for layer in sorted(self.states):
             state = self.states[layer]
-            k = gather_tokens(state["k"], kept[layer])
-            v = gather_tokens(state["v"], kept[layer])
-            cache.update(k, v, layer)
-            self.states[layer] = {"k": k, "v": v}
+            self.states[layer] = {"k": gather_tokens(state["k"], kept[layer]), "v": gather_tokens(state["v"], kept[layer])}
         self.mode = "decode"
-        return cache
+        return self._cache()
 
     def close(self):
         """Restore the model's previous attention implementation."""
@@ -149,6 +167,72 @@ class EvictionController:
             if getattr(m, "_flash_evict_controller", None) is self:
                 del m._flash_evict_controller
         self.model.set_attn_implementation(self._previous)
+
+
+class StreamingController(EvictionController):
+    """Compacts each layer's K/V during the prefill forward, right after that layer's
+    attention (reference streaming_adapter.py:16-27,55-87): the attention output of every
+    layer stays exact for the next layer, only the stored K/V shrink to `budget` tokens, so
+    the full prompt caches of all layers are never held at once. Run the prompt forward
+    with use_cache=False, then `finish_prefill()` returns the compacted `DynamicCache` for
+    decoding. The kept tokens are those `EvictionController.compress(budget)` keeps.
+    """
+
+    def __init__(self, model, *, backend="fused", budget=1024, scoring=None, reserved_recent=64, pool_kernel=1,
+                 snap_window=32):
+        if backend not in ("fused", "snap", "full"):
+            raise ValueError("Unsupported backend")
+        if isinstance(budget, bool) or not isinstance(budget, int) or budget < 1:
+            raise ValueError("Positive integer budget required")
+        self.cache_budget = budget
+        super().__init__(model, backend=backend, scoring=scoring, reserved_recent=reserved_recent,
+                         pool_kernel=pool_kernel, snap_window=snap_window)
+
+    def _store(self, layer, state):
+        idx = self._indices(state, self.cache_budget)
+        if idx is None:
+            self.states[layer] = {"k": state["k"], "v": state["v"]}
+        else:
+            self.states[layer] = {"k": gather_tokens(state["k"], idx), "v": gather_tokens(state["v"], idx)}
+
+    def finish_prefill(self):
+        """The compacted `DynamicCache` of every layer; switches to decode mode."""
+        if not self.states:
+            raise RuntimeError("finish_prefill needs a prefill forward first")
+        self.mode = "decode"
+        return self._cache()
+
+    def compress(self, budget):
+        raise RuntimeError("StreamingController compacts during the prefill forward; call finish_prefill()")
+
+
+def chunk_mlp(model, chunk_size):
+    """Run every decoder layer's MLP over at most `chunk_size` positions at a time, bounding
+    the feed-forward activation memory of long prompts (reference streaming_adapter.py:30-51).
+    Inference only. Returns a function that restores the original MLP forwards."""
+    if isinstance(chunk_size, bool) or not isinstance(chunk_size, int) or chunk_size < 1:
+        raise ValueError("chunk_size must be a positive integer")
+    saved = []
+
+    def chunked(forward):
+        def run(hidden):
+            if torch.is_grad_enabled():
+                raise RuntimeError("Chunked MLP is inference-only")
+            n = hidden.shape[1]
+            if n <= chunk_size:
+                return forward(hidden)
+            parts = [forward(hidden[:, i:i + chunk_size]) for i in range(0, n, chunk_size)]
+            return torch.cat(parts, dim=1)
+        return run
+
+    for layer in model.model.layers:
+        saved.append((layer.mlp, layer.mlp.forward))
+        layer.mlp.forward = chunked(layer.mlp.forward)
+
+    def restore():
+        for mlp, forward in saved:
+            mlp.forward = forward
+    return restore
 
 
 def choose_indices(method, k, v, importance=None, snap=None):

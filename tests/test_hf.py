@@ -1,9 +1,10 @@
 """CPU checks of the transformers integration's host logic: the evaluation policies'
-index choice (reference tests/test_quality_adapter.py:17-24, known answers) and the budget
-parsing of compress (kv_distill_adapter.py:31-33)."""
+index choice (reference tests/test_quality_adapter.py:17-24, known answers), the budget
+parsing of compress (kv_distill_adapter.py:31-33), the streaming controller's argument checks
+and chunk_mlp (reference tests/test_streaming_adapter.py:62-76, here on the CPU)."""
 import torch
 
-from flash_evict.hf import _budget, choose_indices
+from flash_evict.hf import StreamingController, _budget, choose_indices, chunk_mlp
 
 
 def test_ablation_selection_is_exact():
@@ -23,3 +24,53 @@ def test_budget_parsing():
     assert _budget("full", 137) == 137
     assert _budget("500", 137) == 137
     assert _budget("0.001", 137) == 1
+
+
+def _tiny_cpu_model(layers=2):
+    import transformers
+    cfg = transformers.Qwen2Config(vocab_size=257, hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                                   num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(3)
+    return transformers.Qwen2ForCausalLM(cfg).eval()
+
+
+def test_streaming_controller_rejects_bad_arguments():
+    # streaming_adapter.py:19-20 (checked before the model is touched)
+    for kwargs, msg in [(dict(backend="h2o"), "Unsupported backend"), (dict(budget=0), "Positive integer budget"),
+                        (dict(budget=True), "Positive integer budget"), (dict(budget=2.0), "Positive integer budget")]:
+        try:
+            StreamingController(None, **kwargs)
+        except ValueError as e:
+            assert msg in str(e)
+        else:
+            raise AssertionError(kwargs)
+
+
+def test_chunk_mlp_matches_and_restores():
+    # streaming_adapter.py:30-51, on the CPU in float32
+    model = _tiny_cpu_model()
+    ids = torch.randint(0, 257, (1, 75), generator=torch.Generator().manual_seed(1))
+    with torch.inference_mode():
+        expected = model.model(ids, use_cache=False).last_hidden_state
+        restore = chunk_mlp(model, 31)
+        actual = model.model(ids, use_cache=False).last_hidden_state
+        torch.testing.assert_close(actual, expected, atol=1e-5, rtol=1e-5)
+        restore()
+        assert torch.equal(model.model(ids, use_cache=False).last_hidden_state, expected)
+    restore = chunk_mlp(model, 8)
+    try:
+        with torch.enable_grad():
+            model.model(ids, use_cache=False)
+    except RuntimeError as e:
+        assert "inference-only" in str(e)
+    else:
+        raise AssertionError("grad-enabled chunked MLP must raise")
+    restore()
+    for bad in (0, -3, True, 2.5):
+        try:
+            chunk_mlp(model, bad)
+        except ValueError as e:
+            assert "positive integer" in str(e)
+        else:
+            raise AssertionError(bad)

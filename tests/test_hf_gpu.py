@@ -3,11 +3,13 @@ tests' configuration, tests/test_adapter.py and tests/test_streaming_adapter.py)
 fused-prefill model matches the SDPA model (the reference's tolerance, atol .025 rtol .02),
 importance is recorded per layer (H2O mass sums to G*N per KV head), compaction keeps the
 budget with the reserved suffix and only original (RoPE-rotated) keys, and decoding from
-the compacted cache works; with the full budget it reproduces uncompressed decoding."""
+the compacted cache works; with the full budget it reproduces uncompressed decoding. The
+streaming controller (per-layer compaction during the forward) keeps exactly what delayed
+compaction keeps (reference tests/test_streaming_adapter.py)."""
 import pytest
 import torch
 
-from flash_evict.hf import EvictionController
+from flash_evict.hf import EvictionController, StreamingController, chunk_mlp
 
 pytestmark = pytest.mark.gpu
 
@@ -94,3 +96,74 @@ def test_snap_backend_budget():
     for state in ctl.states.values():
         assert state["k"].shape[2] == 48
     ctl.close()
+
+
+def _decode_one(model, ids, cache, n_prompt, kept):
+    return model.model(ids[:, -1:], position_ids=torch.tensor([[n_prompt]], device="cuda"), past_key_values=cache,
+                       use_cache=True, cache_position=torch.tensor([kept], device="cuda")).last_hidden_state
+
+
+# reference tests/test_streaming_adapter.py:9-35: compacting each layer during the forward
+# equals compacting all layers after it, and decoding from either cache agrees
+@torch.inference_mode()
+@pytest.mark.parametrize("scoring", [{"recency_decay": .1}, {"observation_window": 128}])
+def test_immediate_layer_compaction_matches_delayed_compaction(scoring):
+    torch.manual_seed(190)
+    model = tiny_model(3)
+    ids = torch.randint(0, 257, (1, 137), device="cuda")
+    pos = torch.arange(137, device="cuda")[None]
+    ctl = EvictionController(model, scoring=scoring, reserved_recent=16)
+    delayed = model.model(ids, position_ids=pos, use_cache=False).last_hidden_state
+    cache = ctl.compress(48)
+    states = {i: {k: t.clone() for k, t in s.items()} for i, s in ctl.states.items()}
+    decode = _decode_one(model, ids, cache, 137, 48)
+    ctl.close()
+    ctl = StreamingController(model, budget=48, scoring=scoring, reserved_recent=16)
+    immediate = model.model(ids, position_ids=pos, use_cache=False).last_hidden_state
+    assert torch.equal(immediate, delayed)
+    for i, state in ctl.states.items():
+        assert set(state) == {"k", "v"}
+        for key, tensor in state.items():
+            assert torch.equal(tensor, states[i][key])
+    actual = _decode_one(model, ids, ctl.finish_prefill(), 137, 48)
+    assert torch.equal(actual, decode)
+    ctl.close()
+    assert model.config._attn_implementation == "sdpa"
+
+
+# reference tests/test_streaming_adapter.py:38-59
+@torch.inference_mode()
+@pytest.mark.parametrize("backend", ["full", "snap"])
+def test_streaming_baselines_match_delayed(backend):
+    torch.manual_seed(17)
+    model = tiny_model()
+    ids = torch.randint(0, 257, (1, 137), device="cuda")
+    native = model.model(ids, use_cache=False).last_hidden_state
+    ctl = EvictionController(model, backend=backend)
+    expected = model.model(ids, use_cache=False).last_hidden_state
+    ctl.compress(48 if backend == "snap" else 137)
+    states = {i: {k: t.clone() for k, t in s.items()} for i, s in ctl.states.items()}
+    ctl.close()
+    ctl = StreamingController(model, backend=backend, budget=48)
+    actual = model.model(ids, use_cache=False).last_hidden_state
+    torch.testing.assert_close(actual, native, atol=.025, rtol=.02)
+    assert torch.equal(actual, expected)
+    for i, state in ctl.states.items():
+        assert set(state) == {"k", "v"}
+        assert state["k"].shape[2] == (48 if backend == "snap" else 137)
+        for key, tensor in state.items():
+            assert torch.equal(tensor, states[i][key])
+    ctl.close()
+
+
+# reference tests/test_streaming_adapter.py:62-76
+@torch.inference_mode()
+def test_chunked_mlp_and_restore():
+    model = tiny_model()
+    ids = torch.randint(0, 257, (1, 137), device="cuda")
+    expected = model.model(ids, use_cache=False).last_hidden_state
+    restore = chunk_mlp(model, 31)
+    actual = model.model(ids, use_cache=False).last_hidden_state
+    torch.testing.assert_close(actual, expected, atol=.025, rtol=.02)
+    restore()
+    assert torch.equal(model.model(ids, use_cache=False).last_hidden_state, expected)
