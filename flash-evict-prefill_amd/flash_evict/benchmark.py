@@ -22,6 +22,13 @@ Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-hea
 `--kernels` instead times the HBM-bound kernels on scaled synthetics (the headline's score
 array is only 1 MiB, where they are launch-latency bound) and reports achieved GB/s against
 algorithmic bytes (each input byte read once, each output byte written once).
+
+`--policies` runs the protocol of the reference's scripts/benchmark_policies.py:26-96: for
+every length, torch_flash and hip_attention_only once, then per budget flash_snap at windows
+32 and 128 and `evict(budget, **policy)` for every scoring policy (a JSON list of
+{name, recency_decay, observation_window, value_weighted, reserved_recent, pool_kernel} via
+`--policy-file`, else DEFAULT_POLICIES, the reference's published rows), in a seeded
+shuffled order, appending to an existing report with the same arguments (resumable).
 """
 import argparse
 import gc
@@ -118,6 +125,83 @@ def methods_for(q, k, v, budget):
     }
 
 
+# Scoring policies of the reference's published policy benchmark (results/policy_benchmark.json
+# rows d01_r0 and d0.1_w128_*), plus the decay-1 and window-128 policies of its sweep.
+DEFAULT_POLICIES = [
+    dict(name="d01_r0", recency_decay=.1, observation_window=0, value_weighted=True, reserved_recent=0, pool_kernel=1),
+    dict(name="d0.1_w128_r0", recency_decay=.1, observation_window=128, value_weighted=True, reserved_recent=0,
+         pool_kernel=1),
+    dict(name="d0.1_w128_r64", recency_decay=.1, observation_window=128, value_weighted=True, reserved_recent=64,
+         pool_kernel=1),
+    dict(name="w128_r64", recency_decay=0., observation_window=128, value_weighted=True, reserved_recent=64,
+         pool_kernel=1),
+    dict(name="d1_r64", recency_decay=1., observation_window=0, value_weighted=True, reserved_recent=64,
+         pool_kernel=1),
+]
+
+
+def policy_methods(q, k, v, budgets, policies):
+    """(name, budget, callable) of one length (scripts/benchmark_policies.py:58-67)."""
+    methods = [("torch_flash", None, lambda: flash_attention(q, k, v)),
+               ("hip_attention_only", None, lambda: prefill(q, k, v, score=False))]
+    for budget in budgets:
+        for window in (32, 128):
+            methods.append(("snap_w%d" % window, budget, lambda b=budget, w=window: flash_snap(q, k, v, b, w)))
+        for policy in policies:
+            kw = {key: val for key, val in policy.items() if key != "name"}
+            methods.append((policy["name"], budget, lambda b=budget, kw=kw: evict(q, k, v, b, **kw)))
+    return methods
+
+
+def run_policies(args):
+    policies = DEFAULT_POLICIES
+    if args.policy_file:
+        policies = json.loads(Path(args.policy_file).read_text())
+    torch.manual_seed(20260910)
+    dest = Path(args.output)
+    dest.parent.mkdir(parents=True, exist_ok=True)
+    run_args = {"lengths": args.lengths, "budgets": args.budgets, "repeats": args.repeats, "heads": args.heads,
+                "kv_heads": args.kv_heads, "dim": args.dim}
+    report = {"args": run_args, "policies": policies, "gpu": torch.cuda.get_device_name(), "torch": torch.__version__,
+              "hip": torch.version.hip, "dtype": "bfloat16", "batch": 1, "git_revision": _git_revision(),
+              "source_sha256": _sources(),
+              "scope": "one layer; incremental allocations, inputs excluded; output, scores, selection included",
+              "rows": []}
+    if dest.exists():
+        old = json.loads(dest.read_text())
+        for key in ("args", "policies"):
+            if old.get(key) != report[key]:
+                raise ValueError("existing report %s was made with other %s" % (dest, key))
+        report = old
+    done = {(r["n"], r["method"], r["budget"]) for r in report["rows"]}
+    for n in args.lengths:
+        q = torch.randn((1, args.heads, n, args.dim), device="cuda", dtype=torch.bfloat16)
+        k = torch.randn((1, args.kv_heads, n, args.dim), device="cuda", dtype=q.dtype)
+        v = torch.randn_like(k)
+        methods = policy_methods(q, k, v, args.budgets, policies)
+        random.Random(n).shuffle(methods)
+        for name, budget, fn in methods:
+            if (n, name, budget) in done:
+                continue
+            try:
+                row = {"n": n, "method": name, "budget": budget, **measure(fn, args.repeats)}
+            except torch.OutOfMemoryError as e:
+                row = {"n": n, "method": name, "budget": budget, "error": "OOM", "detail": str(e)}
+                gc.collect()
+                torch.cuda.empty_cache()
+            report["rows"].append(row)
+            done.add((n, name, budget))
+            report["kernel_resources"] = kernel_resources()
+            dest.write_text(json.dumps(report, indent=2) + "\n")
+            print(json.dumps({key: val for key, val in row.items() if key != "samples_ms"}), flush=True)
+        del q, k, v
+        gc.collect()
+        torch.cuda.empty_cache()
+    expected = len(args.lengths) * (2 + len(args.budgets) * (2 + len(policies)))
+    report["complete"] = len(done) == expected
+    dest.write_text(json.dumps(report, indent=2) + "\n")
+
+
 def _event_ms(fn, repeats):
     """Median HIP-event time of `fn` (on torch's current stream) after two warm-ups."""
     for _ in range(2):
@@ -180,7 +264,13 @@ def main(argv=None):
     p.add_argument("--methods", nargs="+", default=None, help="subset of the method names")
     p.add_argument("--output", default="benchmark.json")
     p.add_argument("--kernels", action="store_true", help="time the HBM-bound kernels on scaled synthetics")
+    p.add_argument("--policies", action="store_true", help="policy latency at fixed budgets")
+    p.add_argument("--budgets", type=int, nargs="+", default=[256, 1024])
+    p.add_argument("--policy-file", default=None, help="JSON list of scoring policies (--policies)")
     args = p.parse_args(argv)
+    if args.policies:
+        run_policies(args)
+        return
     if args.kernels:
         report = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "hip": torch.version.hip,
                   "rows": kernel_rows(args.repeats)}

@@ -37,3 +37,19 @@ def test_kernel_mode(tmp_path):
     assert [r["kernel"] for r in rows] == ["zero_f32", "select (top-k + mask + indices)", "select with pool 5",
                                           "gather_tokens"]
     assert all(r["median_ms"] > 0 and r["GB/s"] > 0 for r in rows)
+
+
+def test_policy_mode_resumes(tmp_path):
+    out = tmp_path / "p.json"
+    argv = ["--policies", "--lengths", "256", "--budgets", "64", "128", "--heads", "4", "--kv-heads", "2",
+            "--dim", "64", "--repeats", "2", "--output", str(out)]
+    benchmark.main(argv)
+    report = json.loads(out.read_text())
+    rows = report["rows"]
+    expected = {("torch_flash", None), ("hip_attention_only", None)}
+    expected |= {(m, b) for b in (64, 128) for m in ["snap_w32", "snap_w128"] + [p["name"] for p in
+                                                                               benchmark.DEFAULT_POLICIES]}
+    assert {(r["method"], r["budget"]) for r in rows} == expected
+    assert report["complete"] and all(FIELDS <= set(r) for r in rows)
+    benchmark.main(argv)   # resumes: nothing left to measure
+    assert len(json.loads(out.read_text())["rows"]) == len(rows)
