@@ -16,7 +16,8 @@ hands decoding to the upstream attention.
 `StreamingController` compacts each layer's K/V as soon as that layer's prefill attention
 has run (reference streaming_adapter.py:16-87), so the full caches of all layers are never
 held together; `chunk_mlp` bounds the feed-forward activations of long prompts
-(streaming_adapter.py:30-51).
+(streaming_adapter.py:30-51). `PairedController` shares one prefill forward between several
+policies and decodes their caches as one batch (quality_adapter.py:55-136).
 """
 import math
 
@@ -233,6 +234,109 @@ def chunk_mlp(model, chunk_size):
         for mlp, forward in saved:
             mlp.forward = forward
     return restore
+
+
+def default_methods():
+    """The evaluation's policy list (reference quality_adapter.py:19-31): the full cache, SnapKV
+    and three fused policies at budgets 256 and 1024, and two 256-token ablations."""
+    methods = [dict(name="full", backend="full", budget=None)]
+    for budget in (256, 1024):
+        methods.append(dict(name="snap_%d" % budget, backend="snap", budget=budget))
+        for label, window, recent in (("d01_r0", 0, 0), ("d0.1_w128_r0", 128, 0), ("d0.1_w128_r64", 128, 64)):
+            methods.append(dict(name="%s_%d" % (label, budget), backend="fused", budget=budget, recency_decay=.1,
+                                observation_window=window, value_weighted=True, reserved_recent=recent))
+    methods += [dict(name="%s_256" % backend, backend=backend, budget=256)
+                for backend in ("value_norm_only", "uniform_recent")]
+    return methods
+
+
+def group_key(method):
+    """Policies that can share one prefill forward have equal keys (quality_adapter.py:34-37):
+    every baseline uses the same attention output; fused policies need equal scoring."""
+    if method["backend"] != "fused":
+        return ("baseline",)
+    return ("fused", method["recency_decay"], method["observation_window"], method["value_weighted"])
+
+
+class PairedController(EvictionController):
+    """Several eviction policies share one prefill forward, then decode their own compacted
+    caches as one batch (reference quality_adapter.py:55-81,84-112).
+
+    `prepare(methods)` takes policies of one `group_key`. During the prompt forward (run with
+    use_cache=False) every layer computes its attention once, then stores each policy's
+    compacted K/V in `bank[name][layer]` (`choose_indices`). `activate(names)` concatenates the
+    named caches along the batch (equal retained lengths) into a `DynamicCache`, kept as
+    `self.cache`, for `decode_batch`.
+    """
+
+    def __init__(self, model):
+        super().__init__(model, backend="full")
+        self.bank = {}
+        self.active_methods = []
+        self.cache = None
+
+    def prepare(self, methods, length=None):
+        methods = list(methods)
+        if not methods or len({group_key(m) for m in methods}) != 1:
+            raise ValueError("A shared prefill requires identical attention output and score settings")
+        self.reset()
+        self.active_methods = methods
+        self.bank = {m["name"]: {} for m in methods}
+        first = methods[0]
+        if first["backend"] == "fused":
+            self.backend = "fused"
+            self.scoring = {key: first[key] for key in ("recency_decay", "observation_window", "value_weighted")}
+        else:
+            self.backend = "snap" if any(m["backend"] == "snap" for m in methods) else "full"
+            self.scoring = {}
+
+    def _store(self, layer, state):
+        k, v = state["k"], state["v"]
+        for method in self.active_methods:
+            idx = choose_indices(method, k, v, state.get("importance"), state.get("snap"))
+            self.bank[method["name"]][layer] = {"k": k if idx is None else gather_tokens(k, idx),
+                                                "v": v if idx is None else gather_tokens(v, idx)}
+
+    def activate(self, names, *, consume=True):
+        """Batch the named policies' caches (the same retained length) for decoding."""
+        sources = [self.bank[name] for name in names]
+        self.states = {layer: {key: torch.cat([src[layer][key] for src in sources], 0) if len(sources) > 1
+                               else sources[0][layer][key] for key in ("k", "v")} for layer in sources[0]}
+        self.mode = "decode"
+        if consume:
+            for name in names:
+                del self.bank[name]
+        self.cache = self._cache()
+        return self.cache
+
+
+@torch.inference_mode()
+def decode_batch(model, ctl, last_token, prompt_length, max_new_tokens, stop_ids, *, suppress_first_stop=False):
+    """Greedy decoding of every cache of `ctl.activate(...)` from the prompt's last token at
+    position prompt_length-1 (reference quality_adapter.py:115-136); returns the generated
+    ids per batch row, each ending at its first stop id."""
+    cache = ctl.cache
+    batch = next(iter(ctl.states.values()))["k"].shape[0]
+    kept = cache.get_seq_length()
+    device = next(model.parameters()).device
+    token = torch.full((batch, 1), last_token, dtype=torch.long, device=device)
+    generated = [[] for _ in range(batch)]
+    finished = [False] * batch
+    for step in range(max_new_tokens):
+        pos = torch.full((batch, 1), prompt_length - 1 + step, dtype=torch.long, device=device)
+        hidden = model.model(token, position_ids=pos, past_key_values=cache, use_cache=True,
+                             cache_position=torch.tensor([kept + step], device=device)).last_hidden_state
+        logits = model.lm_head(hidden[:, -1])
+        if suppress_first_stop and step == 0:
+            logits[:, list(stop_ids)] = -torch.inf
+        token = logits.argmax(-1, keepdim=True)
+        for i, token_id in enumerate(token[:, 0].tolist()):
+            if not finished[i]:
+                generated[i].append(token_id)
+                finished[i] = token_id in stop_ids
+        if all(finished):
+            break
+    return generated
 
 
 def choose_indices(method, k, v, importance=None, snap=None):

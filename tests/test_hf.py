@@ -4,7 +4,7 @@ parsing of compress (kv_distill_adapter.py:31-33), the streaming controller's ar
 and chunk_mlp (reference tests/test_streaming_adapter.py:62-76, here on the CPU)."""
 import torch
 
-from flash_evict.hf import StreamingController, _budget, choose_indices, chunk_mlp
+from flash_evict.hf import PairedController, StreamingController, _budget, choose_indices, chunk_mlp, default_methods, group_key
 
 
 def test_ablation_selection_is_exact():
@@ -74,3 +74,20 @@ def test_chunk_mlp_matches_and_restores():
             assert "positive integer" in str(e)
         else:
             raise AssertionError(bad)
+
+
+def test_policy_groups_and_default_methods():
+    # quality_adapter.py:19-37
+    methods = default_methods()
+    assert [m["name"] for m in methods][:3] == ["full", "snap_256", "d01_r0_256"]
+    assert len(methods) == 1 + 2 * 4 + 2
+    fused = [m for m in methods if m["backend"] == "fused"]
+    assert {group_key(m) for m in fused} == {("fused", .1, 0, True), ("fused", .1, 128, True)}
+    assert {group_key(m) for m in methods if m["backend"] != "fused"} == {("baseline",)}
+    ctl = PairedController.__new__(PairedController)   # argument checks only; no model needed
+    try:
+        ctl.prepare([methods[0], fused[0]])
+    except ValueError as e:
+        assert "shared prefill" in str(e)
+    else:
+        raise AssertionError("mixed groups must be rejected")

@@ -9,7 +9,7 @@ compaction keeps (reference tests/test_streaming_adapter.py)."""
 import pytest
 import torch
 
-from flash_evict.hf import EvictionController, StreamingController, chunk_mlp
+from flash_evict.hf import EvictionController, PairedController, StreamingController, chunk_mlp, decode_batch
 
 pytestmark = pytest.mark.gpu
 
@@ -167,3 +167,55 @@ def test_chunked_mlp_and_restore():
     torch.testing.assert_close(actual, expected, atol=.025, rtol=.02)
     restore()
     assert torch.equal(model.model(ids, use_cache=False).last_hidden_state, expected)
+
+
+# reference tests/test_quality_adapter.py:27-52: one shared prefill gives every policy the
+# cache the streaming controller gives it alone
+@torch.inference_mode()
+@pytest.mark.parametrize("backend", ["full", "snap", "fused"])
+def test_shared_prefill_matches_independent_policy(backend):
+    torch.manual_seed(73)
+    model = tiny_model()
+    ids = torch.randint(0, 257, (1, 137), device="cuda")
+    pos = torch.arange(137, device="cuda")[None]
+    scoring = dict(recency_decay=.1, observation_window=128, value_weighted=True)
+    methods = [dict(name="%s_%d" % (backend, b), backend=backend, budget=b, **scoring, reserved_recent=16)
+               for b in (32, 48)]
+    paired = PairedController(model)
+    paired.prepare(methods, 137)
+    actual = model.model(ids, position_ids=pos, use_cache=False).last_hidden_state
+    bank = paired.bank
+    paired.close()
+    for method in methods:
+        ctl = StreamingController(model, backend=backend, budget=method["budget"], scoring=scoring,
+                                  reserved_recent=16)
+        expected = model.model(ids, position_ids=pos, use_cache=False).last_hidden_state
+        assert torch.equal(actual, expected)
+        for layer, state in ctl.states.items():
+            for key in ("k", "v"):
+                assert torch.equal(bank[method["name"]][layer][key], state[key])
+        ctl.close()
+
+
+# reference tests/test_quality_adapter.py:55-76
+@torch.inference_mode()
+def test_batched_decode_matches_independent_caches():
+    torch.manual_seed(91)
+    model = tiny_model()
+    ids = torch.randint(0, 257, (1, 137), device="cuda")
+    ctl = PairedController(model)
+    methods = [dict(name=name, backend=name, budget=48) for name in ("uniform_recent", "value_norm_only", "snap")]
+    ctl.prepare(methods, 136)
+    model.model(ids[:, :-1], position_ids=torch.arange(136, device="cuda")[None], use_cache=False)
+    bank = {name: {i: {k: t.clone() for k, t in state.items()} for i, state in states.items()}
+            for name, states in ctl.bank.items()}
+    names = [m["name"] for m in methods]
+    ctl.activate(names)
+    batched = decode_batch(model, ctl, int(ids[0, -1]), 137, 8, set())
+    assert len(batched) == 3 and all(len(g) == 8 for g in batched)
+    for name, actual in zip(names, batched):
+        ctl.bank = {name: bank[name]}
+        ctl.activate([name])
+        expected = decode_batch(model, ctl, int(ids[0, -1]), 137, 8, set())[0]
+        assert actual == expected
+    ctl.close()
