@@ -47,6 +47,8 @@ def _attention(module, query, key, value, attention_mask, scaling=None, dropout=
     if query.shape[0] != 1:
         raise ValueError("flash_evict prefill expects one unpadded prompt at a time")
     layer = module.layer_idx
+    if ctl.inference_transform is not None:   # kv_distill_adapter.py:62-63
+        key, value = ctl.inference_transform(layer, key, value)
     if ctl.backend == "fused":
         out, importance = prefill(query, key, value, scale=scaling, **ctl.scoring)
         ctl._store(layer, {"k": key, "v": value, "importance": importance})
@@ -88,7 +90,9 @@ class EvictionController:
     `snap_window` queries, torch SDPA attention) or "full" (no scoring; compaction keeps
     everything). `scoring` holds prefill keyword arguments (recency_decay,
     observation_window, value_weighted). Use `mode = "prefill"` (the default after
-    construction) for the prompt forward, then `compress`.
+    construction) for the prompt forward, then `compress`. `inference_transform`, when set,
+    is called as f(layer_idx, k, v) -> (k, v) on each layer's prompt K/V before attention and
+    scoring (the reference's Controller hook, kv_distill_adapter.py:62-63).
     """
 
     def __init__(self, model, *, backend="fused", scoring=None, reserved_recent=0, pool_kernel=1, snap_window=32):
@@ -103,6 +107,7 @@ class EvictionController:
         self.snap_window = snap_window
         self.states = {}
         self.mode = "prefill"
+        self.inference_transform = None
         self._previous = model.config._attn_implementation
         self._modules = [m for m in model.modules() if hasattr(m, "layer_idx") and hasattr(m, "q_proj")]
         for m in self._modules:

@@ -39,6 +39,8 @@ def test_qwen_prefill_compress_decode(scoring, recent):
     cache = ctl.compress("fused_0.1")
     for i, state in ctl.states.items():
         assert state["k"].shape[2] == 14 and set(state) == {"k", "v"}
+        # a compact tensor of its own, not a view into the prompt cache
+        assert state["k"].untyped_storage().nbytes() == state["k"].numel() * state["k"].element_size()
         if recent:
             assert torch.equal(state["k"][:, :, -recent:], original[i][:, :, -recent:])
         # every compacted key is a key at its original (already RoPE-rotated) position
@@ -218,4 +220,23 @@ def test_batched_decode_matches_independent_caches():
         ctl.activate([name])
         expected = decode_batch(model, ctl, int(ids[0, -1]), 137, 8, set())[0]
         assert actual == expected
+    ctl.close()
+
+
+@torch.inference_mode()
+def test_inference_transform_applies_before_scoring():
+    torch.manual_seed(23)
+    model = tiny_model()
+    ids = torch.randint(0, 257, (1, 100), device="cuda")
+    ctl = EvictionController(model)
+    model.model(ids, use_cache=False)
+    plain = {i: s["importance"].clone() for i, s in ctl.states.items()}
+    v0 = ctl.states[0]["v"].clone()
+    ctl.reset()
+    ctl.inference_transform = lambda layer, k, v: (k, v * 2 if layer == 0 else v)
+    model.model(ids, use_cache=False)
+    # layer 0 sees V doubled (exact in bf16): P is unchanged and the value L1 norms double, so
+    # its importance doubles (up to FP32 atomic order)
+    assert torch.equal(ctl.states[0]["v"], v0 * 2)
+    torch.testing.assert_close(ctl.states[0]["importance"], plain[0] * 2, rtol=1e-5, atol=1e-6)
     ctl.close()
