@@ -244,13 +244,14 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     }
 
     if (kb + BN - 1 > lo_lim) {
+      // key kb + 32s + 8(i/4) + 4h + i%4 is visible iff its offset within the tile is at most
+      // rel: one subtraction per lane, then compares against inline constants
+      const int rel = qlim - kb - 4 * hh;
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + 32 * s + 8 * (i >> 2) + 4 * hh + (i & 3);
-          sacc[s][i] = key <= qlim ? sacc[s][i] : NEG_INF;
-        }
+        for (int i = 0; i < 16; ++i)
+          sacc[s][i] = 32 * s + 8 * (i >> 2) + (i & 3) <= rel ? sacc[s][i] : NEG_INF;
     }
     // max over the 32 keys of this lane (four chains, then a tree) and the other half-wave
     float m4[4];
@@ -416,12 +417,10 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
       if (a.causal && kb + BN - 1 > q0) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const int key = kb + 32 * s + l32;
+          // key kb + 32s + l32 against row q0 + 8(i/4) + 4h + i%4
+          const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int qr = q0 + 8 * (i >> 2) + 4 * hh + (i & 3);
-            sacc[s][i] = key > qr ? NEG_INF : sacc[s][i];
-          }
+          for (int i = 0; i < 16; ++i) sacc[s][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[s][i];
         }
       }
 #pragma unroll
