@@ -2,8 +2,10 @@
 // 16-byte K/V rows. Same mathematics as the generic kernel in fe_attn.hip (reference
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
 //
-//   * A workgroup is 8 waves of one 32-query row tile each, all on one KV head (GQA
-//     packing), so each K/V tile in LDS serves 8 row tiles; waves 0-3 issue the DMA.
+//   * A workgroup is NW waves of one 32-query row tile each, all on one KV head (GQA
+//     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. The
+//     attention-only kernel at D = 128 runs 12 waves, three per SIMD; the kernel with the
+//     fused replay traversal, and D = 64, run 8.
 //   * The K/V buffers hold pairs of 64-key tiles: one barrier per 128 keys.
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
@@ -57,7 +59,6 @@ struct FastTile {
   static constexpr int DMA_PER_WAVE = (BN * CPR) / 256;
   static constexpr int NDC = DP / 16;            // MFMA k-chunks of QK^T
   static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
-  static constexpr int NW = 8;                   // waves (row tiles) per workgroup
 };
 
 // XOR applied to the 16-byte chunk index of row `key`. Two read patterns must be bank-
@@ -84,10 +85,29 @@ __device__ __forceinline__ float half_swap_maximum(float x) {
   return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// DMA of one 64-key tile: wave wv moves 1 KB blocks wv, wv+4, ...; lane l of a block fills
-// LDS chunk (block*64 + l) with the global chunk that the swizzle puts there (per-lane
-// offsets `doff`). The tile's first row enters through the buffer base and the record count
-// ends at row N, so rows past N read as zero.
+// DMA of one 64-key tile with one per-lane offset register (fused_fast_kernel): wave wv
+// moves 1 KB blocks wv, wv+4, ...; lane l of a block fills LDS chunk (block*64 + l) with the
+// global chunk that the swizzle puts there. Block r of the tile (its keys start at
+// kb + r*KSTEP, KSTEP = 256 / chunks per row) gets a buffer descriptor of its own whose base
+// and record count start at that key. The block's per-lane offsets then equal block 0's
+// (the swizzle depends on key bits 0..3 only, which r*KSTEP does not change), and every
+// access stays range checked: rows past N read as zero.
+template <int DPW, int KSTEP>
+__device__ __forceinline__ void dma_tile1(const unsigned char* g, u32 rowb, u32 doff0, int kb, int N,
+                                          unsigned char* ldst, int wv) {
+#pragma unroll
+  for (int r = 0; r < DPW; ++r) {
+    const int k0 = kb + r * KSTEP;
+    const int nrec = N > k0 ? (int)((u32)(N - k0) * rowb) : 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g + (size_t)k0 * rowb), (short)0, nrec, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(ldst + (r * 4 + wv) * 1024), 16, doff0, 0, 0, 0);
+  }
+}
+
+// The same DMA with one offset register per block (replay_fast_kernel): the tile's first row
+// enters through the buffer base and the record count ends at row N, so rows past N read as
+// zero.
 template <int DPW>
 __device__ __forceinline__ void dma_tile(const unsigned char* g, u32 rowb, const u32* doff, int kb, int N,
                                          unsigned char* ldst, int wv) {
@@ -98,11 +118,17 @@ __device__ __forceinline__ void dma_tile(const unsigned char* g, u32 rowb, const
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(ldst + (r * 4 + wv) * 1024), 16, doff[r], 0, 0, 0);
 }
 
-template <typename E, int DP>
-__global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(const AttnArgs a) {
+// NW waves of one row tile each (8: two waves per SIMD; 12: three, for the attention-only
+// variant at D = 128, which then reads K fragments in two halves and V fragments without
+// prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
+// workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
+template <typename E, int DP, int NW, bool FUSED>
+__global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
-  constexpr int DPW = T::DMA_PER_WAVE, NW = T::NW;
+  constexpr int DPW = T::DMA_PER_WAVE;
+  constexpr int KH = NW > 8 ? 2 : 1;             // K fragment reads per 32-key half
+  static_assert(NW % 2 == 0 && NW >= 4, "row tiles per workgroup");
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -112,7 +138,7 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
   // Two buffers per operand, each holding two consecutive 64-key tiles (slots 0 and 1).
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[2 * TILE], lds_k1[2 * TILE], lds_v0[2 * TILE],
       lds_v1[2 * TILE];
-  __shared__ float red[2 * NW * BN];             // [2][NW][BN] per-wave column sums
+  __shared__ float red[FUSED ? 2 * NW * BN : 1];  // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -171,28 +197,28 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
       }
   }
 
-  // Per-lane global offsets of the tile DMA (fixed; see dma_tile).
+  // Per-lane global offsets of the tile DMA, fixed (see dma_tile1): lane l of wave w fills
+  // LDS chunk w*64 + l of every 1 KB block from key (w*64 + l) / CPR of the block.
   const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
-  u32 dk[DPW], dv[DPW];
-#pragma unroll
-  for (int r = 0; r < DPW; ++r) {
-    const int c = (r * 4 + (wv & 3)) * 64 + lane;
+  u32 dk, dv;
+  {
+    const int c = (wv & 3) * 64 + lane;
     const int key = c / CPR, pc = c % CPR;
     const u32 lc = (u32)(pc ^ swz<DP>(key));
-    dk[r] = (u32)key * krow + lc * 16u;
-    dv[r] = (u32)key * vrow + lc * 16u;
+    dk = (u32)key * krow + lc * 16u;
+    dv = (u32)key * vrow + lc * 16u;
   }
   const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
   const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
-  auto dma = [&](const unsigned char* g, u32 rowb, const u32(&doff)[DPW], int kb, unsigned char* ldst) {
-    dma_tile<DPW>(g, rowb, doff, kb, N, ldst, wv);
+  auto dma = [&](const unsigned char* g, u32 rowb, u32 doff, int kb, unsigned char* ldst) {
+    dma_tile1<DPW, 256 / CPR>(g, rowb, doff, kb, N, ldst, wv);
   };
 
-  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT
-  auto k_frags = [&](int BUF, int SLOT, int s, u32x4(&kf)[NDC]) __attribute__((always_inline)) {
+  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunks h*NDC/KH .. +NDC/KH
+  auto k_frags = [&](int BUF, int SLOT, int s, int h, u32x4(&kf)[NDC / KH]) __attribute__((always_inline)) {
     const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) kf[c] = *(const u32x4*)(kt + koff[c] + s * 32 * ROWB);
+    for (int c = 0; c < NDC / KH; ++c) kf[c] = *(const u32x4*)(kt + koff[h * (NDC / KH) + c] + s * 32 * ROWB);
   };
   // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT (two transposing
   // reads)
@@ -234,13 +260,18 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     f32x16 sacc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      u32x4 kf[NDC];
-      k_frags(BUF, SLOT, s, kf);
-      FE_PRIO_HI();
-      sacc[s] = E::mfma(kf[0], qf[0], (f32x16){});
 #pragma unroll
-      for (int c = 1; c < NDC; ++c) sacc[s] = E::mfma(kf[c], qf[c], sacc[s]);
-      FE_PRIO_LO();
+      for (int h = 0; h < KH; ++h) {
+        u32x4 kf[NDC / KH];
+        k_frags(BUF, SLOT, s, h, kf);
+        FE_PRIO_HI();
+#pragma unroll
+        for (int c = 0; c < NDC / KH; ++c) {
+          const int cc = h * (NDC / KH) + c;
+          sacc[s] = cc == 0 ? E::mfma(kf[c], qf[0], (f32x16){}) : E::mfma(kf[c], qf[cc], sacc[s]);
+        }
+        FE_PRIO_LO();
+      }
     }
 
     if (kb + BN - 1 > lo_lim) {
@@ -296,20 +327,34 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
-    // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
-    u32x4 vf[2][4];
+    if constexpr (NW > 8) {
+      // three waves per SIMD cover the V read latency; no prefetch (16 fewer registers)
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
+      for (int dt = 0; dt < NDT; ++dt) {
+        u32x4 vf[4];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      if (dt + 1 < NDT) {
+        for (int c4 = 0; c4 < 4; ++c4) vf[c4] = v_frag(BUF, SLOT, c4, dt);
+        FE_PRIO_HI();
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
+        for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[c4], pb[c4], o[dt]);
+        FE_PRIO_LO();
       }
-      FE_PRIO_HI();
+    } else {
+      // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
+      u32x4 vf[2][4];
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[dt & 1][c4], pb[c4], o[dt]);
-      FE_PRIO_LO();
+      for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        if (dt + 1 < NDT) {
+#pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
+        }
+        FE_PRIO_HI();
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[dt & 1][c4], pb[c4], o[dt]);
+        FE_PRIO_LO();
+      }
     }
   };
 
@@ -364,97 +409,99 @@ __global__ __launch_bounds__(FastTile<DP>::NW * 64, 2) void fused_fast_kernel(co
     }
     return;
   }
-  if (wg_q_hi - 1 < a.win_lo) return;
+  if constexpr (FUSED) {
+    if (wg_q_hi - 1 < a.win_lo) return;
 
-  // p_qk * w_q / l_q = exp2(s*scale - b_q) with b_q = m_q + log2 l_q - decay*log2e*(q-N+1),
-  // b_q = +inf for rows outside the window or past N. nb holds -b of the 16 rows of a lane.
-  float nb[16];
-  {
-    const int qi = q0 + l32;
-    const bool live = tv && qi < N && qi >= a.win_lo;
-    const float br = live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
-  }
-  const bool rin = tv && q0 + 31 >= a.win_lo;
-  const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
-  float* imp_row = a.imp + (long long)bh * N;
-
-  // Flush of the previous tile's per-wave column sums (written before the barrier that
-  // precedes this call): one atomic per key per workgroup.
-  auto flush = [&](int kb_prev, int buf_prev) {
-    if (tid < BN) {
-      const float* rr = red + buf_prev * NW * BN + tid;
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
-      const int key = kb_prev + tid;
-      if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+    // p_qk * w_q / l_q = exp2(s*scale - b_q) with b_q = m_q + log2 l_q - decay*log2e*(q-N+1),
+    // b_q = +inf for rows outside the window or past N. nb holds -b of the 16 rows of a lane.
+    float nb[16];
+    {
+      const int qi = q0 + l32;
+      const bool live = tv && qi < N && qi >= a.win_lo;
+      const float br = live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
     }
-  };
+    const bool rin = tv && q0 + 31 >= a.win_lo;
+    const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
+    float* imp_row = a.imp + (long long)bh * N;
 
-  // One 64-key tile: S = Q K^T (lanes hold keys), causal mask on diagonal tiles, column
-  // sums of exp2(S*scale - b_q) over this wave's 32 rows, written to LDS for the flush.
-  auto t2_step = [&](int it, int BUF) __attribute__((always_inline)) {
-    const int kb = it * BN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (it > 0) flush(kb - BN, BUF ^ 1);
-    if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
-    float cs[2] = {0.f, 0.f};
-    if (kb <= wave_hi_r) {
-      f32x16 sacc[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4 kf[NDC];
-        k_frags(BUF, 0, s, kf);
-        FE_PRIO_HI();
-        sacc[s] = E::mfma(qf[0], kf[0], (f32x16){});
-#pragma unroll
-        for (int c = 1; c < NDC; ++c) sacc[s] = E::mfma(qf[c], kf[c], sacc[s]);
-        FE_PRIO_LO();
+    // Flush of the previous tile's per-wave column sums (written before the barrier that
+    // precedes this call): one atomic per key per workgroup.
+    auto flush = [&](int kb_prev, int buf_prev) {
+      if (tid < BN) {
+        const float* rr = red + buf_prev * NW * BN + tid;
+        float sum = 0.f;
+  #pragma unroll
+        for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
+        const int key = kb_prev + tid;
+        if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
       }
-      if (a.causal && kb + BN - 1 > q0) {
-#pragma unroll
+    };
+
+    // One 64-key tile: S = Q K^T (lanes hold keys), causal mask on diagonal tiles, column
+    // sums of exp2(S*scale - b_q) over this wave's 32 rows, written to LDS for the flush.
+    auto t2_step = [&](int it, int BUF) __attribute__((always_inline)) {
+      const int kb = it * BN;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (it > 0) flush(kb - BN, BUF ^ 1);
+      if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
+      float cs[2] = {0.f, 0.f};
+      if (kb <= wave_hi_r) {
+        f32x16 sacc[2];
+  #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          // key kb + 32s + l32 against row q0 + 8(i/4) + 4h + i%4
-          const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) sacc[s][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[s][i];
+          u32x4 kf[NDC];
+          k_frags(BUF, 0, s, 0, kf);
+          FE_PRIO_HI();
+          sacc[s] = E::mfma(qf[0], kf[0], (f32x16){});
+  #pragma unroll
+          for (int c = 1; c < NDC; ++c) sacc[s] = E::mfma(qf[c], kf[c], sacc[s]);
+          FE_PRIO_LO();
+        }
+        if (a.causal && kb + BN - 1 > q0) {
+  #pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            // key kb + 32s + l32 against row q0 + 8(i/4) + 4h + i%4
+            const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[s][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[s][i];
+          }
+        }
+  #pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          float c4[4];
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float e = fast_exp2(fmaf(sacc[s][i], a.scale_log2, nb[i]));
+            if (i < 4)
+              c4[i] = e;
+            else
+              c4[i & 3] += e;
+          }
+          cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
         }
       }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float c4[4];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(fmaf(sacc[s][i], a.scale_log2, nb[i]));
-          if (i < 4)
-            c4[i] = e;
-          else
-            c4[i & 3] += e;
-        }
-        cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+      cs[0] = half_swap_sum(cs[0]);
+      cs[1] = half_swap_sum(cs[1]);
+      if (hh == 0) {
+        float* rb = red + BUF * NW * BN + wv * BN;
+        rb[l32] = cs[0];
+        rb[32 + l32] = cs[1];
       }
-    }
-    cs[0] = half_swap_sum(cs[0]);
-    cs[1] = half_swap_sum(cs[1]);
-    if (hh == 0) {
-      float* rb = red + BUF * NW * BN + wv * BN;
-      rb[l32] = cs[0];
-      rb[32 + l32] = cs[1];
-    }
-  };
+    };
 
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();  // every wave is done reading the traversal-1 tiles
-  if (dmaw) dma(kg, krow, dk, 0, lds_k0);
-  for (int it = 0; it < ntiles; it += 2) {
-    t2_step(it, 0);
-    if (it + 1 < ntiles) t2_step(it + 1, 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave is done reading the traversal-1 tiles
+    if (dmaw) dma(kg, krow, dk, 0, lds_k0);
+    for (int it = 0; it < ntiles; it += 2) {
+      t2_step(it, 0);
+      if (it + 1 < ntiles) t2_step(it + 1, 1);
+    }
+    __syncthreads();
+    flush((ntiles - 1) * BN, (ntiles - 1) & 1);
   }
-  __syncthreads();
-  flush((ntiles - 1) * BN, (ntiles - 1) & 1);
 }
 
 // Replay traversal of the split schedule. After fused_fast_kernel has written the bias
@@ -636,16 +683,24 @@ ReplayPlan g_replay[] = {
     replay_entry<BF16, 128>("replay_fast<bf16,128>"),
 };
 
-template <typename E, int DP>
+template <typename E, int DP, int NW, bool FUSED>
 FusedPlan fast_entry(const char* name) {
-  return FusedPlan{(const void*)fused_fast_kernel<E, DP>, 0, FastTile<DP>::NW, FastTile<DP>::NW, name};   // static LDS only
+  return FusedPlan{(const void*)fused_fast_kernel<E, DP, NW, FUSED>, 0, NW, NW, name};   // static LDS only
 }
 
+// Per (dtype, D): the attention-only kernel (split schedule, or no importance) and the fused
+// kernel with the replay traversal (fe_prefill without a workspace). At D = 64 the
+// attention-only kernel stays at 8 waves: 125 registers and 68 KiB of LDS already put two
+// workgroups, four waves per SIMD, on a CU.
 FusedPlan g_fast[] = {
-    fast_entry<F16, 64>("fused_fast<f16,64>"),
-    fast_entry<F16, 128>("fused_fast<f16,128>"),
-    fast_entry<BF16, 64>("fused_fast<bf16,64>"),
-    fast_entry<BF16, 128>("fused_fast<bf16,128>"),
+    fast_entry<F16, 64, 8, false>("attn_fast<f16,64>"),
+    fast_entry<F16, 64, 8, true>("fused_fast<f16,64>"),
+    fast_entry<F16, 128, 12, false>("attn_fast<f16,128>"),
+    fast_entry<F16, 128, 8, true>("fused_fast<f16,128>"),
+    fast_entry<BF16, 64, 8, false>("attn_fast<bf16,64>"),
+    fast_entry<BF16, 64, 8, true>("fused_fast<bf16,64>"),
+    fast_entry<BF16, 128, 12, false>("attn_fast<bf16,128>"),
+    fast_entry<BF16, 128, 8, true>("fused_fast<bf16,128>"),
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -662,7 +717,8 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   if (a.D != 64 && a.D != 128) return false;
   if (!(a.scale_log2 > 0.f) || !a.qvec) return false;
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
-  const int idx = (dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0);
+  const bool fused = a.score && !a.bias;
+  const int idx = 2 * ((dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0)) + (fused ? 1 : 0);
   plan = g_fast[idx];
   return true;
 }
