@@ -10,13 +10,14 @@
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
 //     (scalar arithmetic only), so rows past N read as zero and no VALU work is spent on
-//     addresses. LDS rows are stored unpadded with the 16-byte chunk index XOR-swizzled by
-//     the key, so fragment reads are bank-conflict free.
-//   * Every LDS read uses a per-lane offset register fixed for the whole kernel plus an
-//     immediate (key half, 16-key group, buffer, slot): the buffers are separate LDS objects
-//     and the tile loop is unrolled over both buffers, so no address arithmetic remains in
-//     the loop, and the waitcount pass can see that the DMA into one buffer does not alias
-//     reads of the other (reads of tiles t, t+1 never wait for the DMA of t+2, t+3).
+//     addresses. The attention kernel stores a tile channel-group-major (K: 32-byte groups,
+//     V: 64-byte groups, each group's 64 rows contiguous), so each operand needs a single
+//     per-lane LDS offset register and the fragment reads are bank-conflict free.
+//   * Every LDS read uses that per-lane register plus an immediate (channel group, key
+//     half, 16-key group, buffer, slot): the buffers are separate LDS objects and the tile
+//     loop is unrolled over both buffers, so no address arithmetic remains in the loop, and
+//     the waitcount pass can see that the DMA into one buffer does not alias reads of the
+//     other (reads of tiles t, t+1 never wait for the DMA of t+2, t+3).
 //   * The A operand of O^T = V^T P^T (eight keys of one channel per lane) comes straight
 //     from the row-major V tile with two ds_read_b64_tr_b16 transposing reads; the key
 //     order of the read matches the S^T accumulator row order that becomes P^T.
@@ -61,16 +62,13 @@ struct FastTile {
   static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
 };
 
-// XOR applied to the 16-byte chunk index of row `key`. Two read patterns must be bank-
-// conflict free (64 banks x 4 B = 256 B per cycle):
-//   K fragments: 16 consecutive keys, one logical chunk per access phase;
-//   V transposing reads: 4 consecutive keys x 4 consecutive chunks (aligned group of 4).
-// Moving the key's two low bits into the chunk's high bits serves both: the 16 keys map to
-// 16 distinct chunks, and the 4 keys of a transposing read land in 4 different chunk
-// groups. For 128-byte rows (D = 64) two rows share a bank cycle, so key bit 0 selects the
-// half and bits 1..3 are spread the same way. Only key bits 0..3 matter, so the swizzle of
-// key k and of k + 16j agree: every per-lane LDS offset is fixed for the whole kernel and
-// the tile, key group and buffer enter as instruction immediates.
+// Row-major K tiles (replay_fast_kernel): XOR applied to the 16-byte chunk index of row
+// `key` so that a K fragment read (16 consecutive keys, one logical chunk per access phase;
+// 64 banks x 4 B = 256 B per cycle) hits 16 distinct chunks: the key's two low bits move
+// into the chunk's high bits. For 128-byte rows (D = 64) two rows share a bank cycle, so
+// key bit 0 selects the half and bits 1..3 are spread the same way. Only key bits 0..3
+// matter, so the swizzle of key k and of k + 16j agree and every per-lane LDS offset is
+// fixed for the whole kernel.
 template <int DP>
 __device__ __forceinline__ int swz(int key) {
   return DP == 128 ? (((key & 3) << 2) | ((key >> 2) & 3)) : ((((key >> 1) & 1) << 2) | ((key >> 2) & 3));
@@ -85,24 +83,35 @@ __device__ __forceinline__ float half_swap_maximum(float x) {
   return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// DMA of one 64-key tile with one per-lane offset register (fused_fast_kernel): wave wv
-// moves 1 KB blocks wv, wv+4, ...; lane l of a block fills LDS chunk (block*64 + l) with the
-// global chunk that the swizzle puts there. Block r of the tile (its keys start at
-// kb + r*KSTEP, KSTEP = 256 / chunks per row) gets a buffer descriptor of its own whose base
-// and record count start at that key. The block's per-lane offsets then equal block 0's
-// (the swizzle depends on key bits 0..3 only, which r*KSTEP does not change), and every
-// access stays range checked: rows past N read as zero.
-template <int DPW, int KSTEP>
-__device__ __forceinline__ void dma_tile1(const unsigned char* g, u32 rowb, u32 doff0, int kb, int N,
-                                          unsigned char* ldst, int wv) {
+// DMA of one 64-key tile in channel-group-major order (fused_fast_kernel). The tile is
+// column groups of GB bytes per row, each stored as 64 consecutive rows of GB bytes; a 1 KB
+// block holds KPB = 1024 / GB rows of one group: block B is group B / BPG, rows
+// (B % BPG) * KPB ... + KPB - 1 (BPG = 64 / KPB blocks per group). Wave wv moves blocks
+// wv + 4r (r < DPW). BPG divides 4, so all of a wave's blocks start at the same row and
+// their groups are 4 / BPG apart, 64 bytes of the global row: one buffer descriptor per wave
+// (base at the first row and group, record count ending at row N) serves them all with
+// soffset = 64r. Lane l fetches the same offset in every block (doff: row l / (GB/16) and
+// a 16-byte chunk of the group), so one offset register serves the whole tile. Rows past N
+// read as zero: a lane's offset reaches row N exactly when its row does, and 64r plus the
+// group width never exceeds the row (64(DPW - 1) + GB <= 2D), so an in-range row is read
+// whole.
+template <int DPW, int GB>
+__device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u32 doff, int kb, int N,
+                                            unsigned char* ldst, int wv) {
+  constexpr int KPB = 1024 / GB, BPG = 64 / KPB;
+  static_assert(4 % BPG == 0 && (4 / BPG) * GB == 64, "one descriptor per wave");
+  // recomputed per call: hoisting the per-block LDS addresses of every call site out of the
+  // tile loop would hold dozens of scalar registers
+  int w = wv;
+  asm volatile("" : "+s"(w));
+  const int k0 = kb + (w % BPG) * KPB;
+  const int nrec = N > k0 ? (int)((u32)(N - k0) * rowb) : 0;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g + (size_t)((u32)k0 * rowb) + (w / BPG) * GB), (short)0, nrec, 0x00020000);
+  unsigned char* dst = ldst + w * 1024;
 #pragma unroll
-  for (int r = 0; r < DPW; ++r) {
-    const int k0 = kb + r * KSTEP;
-    const int nrec = N > k0 ? (int)((u32)(N - k0) * rowb) : 0;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(g + (size_t)k0 * rowb), (short)0, nrec, 0x00020000);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(ldst + (r * 4 + wv) * 1024), 16, doff0, 0, 0, 0);
-  }
+  for (int r = 0; r < DPW; ++r)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + r * 4096), 16, doff, 64 * r, 0, 0);
 }
 
 // The same DMA with one offset register per block (replay_fast_kernel): the tile's first row
@@ -176,62 +185,52 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
     for (int c = 0; c < NDC; ++c) qf[c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
   }
 
-  // Per-lane LDS byte offsets, fixed for the kernel.
-  //   K fragment c of key l32 (keys 32..63: + 32*ROWB; from the K buffer of the tile).
-  //   V^T fragment of channel tile dt: eight keys of channel 32*dt + lane%32 in P^T slot
-  //   order, slots 0-3 = keys 4h + 0..3 and slots 4-7 = keys 8 + 4h + 0..3 (h = lane/32)
-  //   of a 16-key group (group c4: + 16*c4*ROWB; from the V buffer of the tile).
-  u32 koff[NDC];
-#pragma unroll
-  for (int c = 0; c < NDC; ++c) koff[c] = (u32)(l32 * ROWB + (((2 * c + hh) ^ swz<DP>(l32)) << 4));
-  u32 voff[2][NDT];
+  // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
+  // group, buffer and slot enter as instruction immediates.
+  //   K tile: [chunk pair c][64 keys][32 B]. Fragment c of key 32s + l32 is chunk 2c + h
+  //   (h = lane/32) at c*2048 + (32s + l32)*32 + 16*(h ^ key bit 3): the XOR puts keys k and
+  //   k+8 in different halves of the 256-byte bank row, so the 16 lanes of a read phase hit
+  //   every bank once.
+  //   V tile: [channel tile dt][64 keys][64 B], unswizzled: four consecutive keys fill one
+  //   256-byte bank row. The V^T fragment of channel tile dt, 16-key group c4, holds eight
+  //   keys of channel 32dt + lane%32 in P^T slot order: slots 0-3 = keys 4h + 0..3 and slots
+  //   4-7 = keys 8 + 4h + 0..3 (two transposing reads, + 512 B apart).
+  const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+  u32 voff;
   {
     const int r = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int k = 8 * half + 4 * hh + (r >> 2);
-        const int d = 32 * dt + 16 * (g & 1) + 4 * (r & 3);
-        voff[half][dt] = (u32)(k * ROWB + (((d >> 3) ^ swz<DP>(k)) << 4) + (((d >> 2) & 1) << 3));
-      }
+    voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
   }
 
-  // Per-lane global offsets of the tile DMA, fixed (see dma_tile1): lane l of wave w fills
-  // LDS chunk w*64 + l of every 1 KB block from key (w*64 + l) / CPR of the block.
+  // Per-lane global offsets of the tile DMA (dma_tile_cm), the same for every block and
+  // wave: K blocks are 32 keys x 2 chunks (lane l: key l/2, chunk l%2 XOR key bit 3, the
+  // swizzle above), V blocks 16 keys x 4 chunks (lane l: key l/4, chunk l%4).
   const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
-  u32 dk, dv;
-  {
-    const int c = (wv & 3) * 64 + lane;
-    const int key = c / CPR, pc = c % CPR;
-    const u32 lc = (u32)(pc ^ swz<DP>(key));
-    dk = (u32)key * krow + lc * 16u;
-    dv = (u32)key * vrow + lc * 16u;
-  }
+  const u32 dk = (u32)(lane >> 1) * krow + (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
+  const u32 dv = (u32)(lane >> 2) * vrow + (u32)((lane & 3) << 4);
   const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
   const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
-  auto dma = [&](const unsigned char* g, u32 rowb, u32 doff, int kb, unsigned char* ldst) {
-    dma_tile1<DPW, 256 / CPR>(g, rowb, doff, kb, N, ldst, wv);
-  };
+  auto dma_k = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 32>(kg, krow, dk, kb, N, ldst, wv); };
+  auto dma_v = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 64>(vg, vrow, dv, kb, N, ldst, wv); };
 
-  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunks h*NDC/KH .. +NDC/KH
+  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunk pairs h*NDC/KH .. +NDC/KH
   auto k_frags = [&](int BUF, int SLOT, int s, int h, u32x4(&kf)[NDC / KH]) __attribute__((always_inline)) {
-    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
+    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
 #pragma unroll
-    for (int c = 0; c < NDC / KH; ++c) kf[c] = *(const u32x4*)(kt + koff[h * (NDC / KH) + c] + s * 32 * ROWB);
+    for (int c = 0; c < NDC / KH; ++c) kf[c] = *(const u32x4*)(kt + (h * (NDC / KH) + c) * 2048);
   };
-  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT (two transposing
-  // reads)
+  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT
   auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
-    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + 16 * c4 * ROWB;
-    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[0][dt]));
-    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + voff[1][dt]));
+    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
+    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
     const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
     return (u32x4){ux[0], ux[1], uy[0], uy[1]};
   };
 
   f32x16 o[NDT];
   float m_run = NEG_INF, l_run = 0.f;
+  float nm = 0.f;                                // -m_run, or 0 while m_run is -inf
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
 
@@ -245,8 +244,8 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl)
         if (it + 2 + sl < ntiles) {
-          dma(kg, krow, dk, (it + 2 + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
-          dma(vg, vrow, dv, (it + 2 + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+          dma_k((it + 2 + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+          dma_v((it + 2 + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
         }
     }
   };
@@ -284,15 +283,16 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
         for (int i = 0; i < 16; ++i)
           sacc[s][i] = 32 * s + 8 * (i >> 2) + (i & 3) <= rel ? sacc[s][i] : NEG_INF;
     }
-    // max over the 32 keys of this lane (four chains, then a tree) and the other half-wave
-    float m4[4];
+    // max over the 32 keys of this lane and the other half-wave: two chains of three-input
+    // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
+    float mc[2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      m4[q] = vmax(sacc[0][4 * q], sacc[1][4 * q]);
+    for (int s = 0; s < 2; ++s) {
+      mc[s] = vmax(vmax(sacc[s][0], sacc[s][1]), sacc[s][2]);
 #pragma unroll
-      for (int i = 1; i < 4; ++i) m4[q] = vmax(m4[q], vmax(sacc[0][4 * q + i], sacc[1][4 * q + i]));
+      for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
     }
-    const float mr = half_swap_maximum(vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3])));
+    const float mr = half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15])));
     // Exact running max: the dominant probability of a row stays exactly 1 before it is
     // rounded to the input dtype (a stale max would cost up to 2^-9 relative error on the
     // term that dominates a peaked row). O and l are only touched when some row's max rose.
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
       m_run = mn;
+      nm = mn == NEG_INF ? 0.f : -mn;
     }
-    const float nm = m_run == NEG_INF ? 0.f : -m_run;
 
     u32x4 pb[4];
     float ps[4];
@@ -362,8 +362,8 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
       if (sl < ntiles) {
-        dma(kg, krow, dk, sl * BN, lds_k0 + sl * TILE);
-        dma(vg, vrow, dv, sl * BN, lds_v0 + sl * TILE);
+        dma_k(sl * BN, lds_k0 + sl * TILE);
+        dma_v(sl * BN, lds_v0 + sl * TILE);
       }
   }
   for (int it = 0; it < ntiles; it += 4) {
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (it > 0) flush(kb - BN, BUF ^ 1);
-      if (dmaw && it + 1 < ntiles) dma(kg, krow, dk, kb + BN, BUF == 0 ? lds_k1 : lds_k0);
+      if (dmaw && it + 1 < ntiles) dma_k(kb + BN, BUF == 0 ? lds_k1 : lds_k0);
       float cs[2] = {0.f, 0.f};
       if (kb <= wave_hi_r) {
         f32x16 sacc[2];
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // every wave is done reading the traversal-1 tiles
-    if (dmaw) dma(kg, krow, dk, 0, lds_k0);
+    if (dmaw) dma_k(0, lds_k0);
     for (int it = 0; it < ntiles; it += 2) {
       t2_step(it, 0);
       if (it + 1 < ntiles) t2_step(it + 1, 1);

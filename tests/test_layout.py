@@ -1,6 +1,10 @@
-"""Host-side check of the fast kernel's LDS layout rules (fe_attn_fast.hip `swz`, `k_frag`,
-`v_frag`): the chunk swizzle is a bijection per row, and the two read patterns the kernel
-issues touch distinct bank slots (64 banks x 4 B = 256 B per cycle)."""
+"""Host-side check of the fast kernels' LDS layout rules (fe_attn_fast.hip), 64 banks x 4 B =
+256 B per cycle:
+* the row-major K tiles of replay_fast_kernel (`swz`): the chunk swizzle is a bijection per
+  row and a K fragment read phase touches distinct bank slots;
+* the channel-group-major K and V tiles of fused_fast_kernel (`dma_tile_cm`, `k_frags`,
+  `v_frag`): the DMA writes every LDS byte of a tile once, each fragment read returns the
+  key and channels the MFMA expects, and each read phase touches distinct bank slots."""
 import pytest
 
 
@@ -27,18 +31,59 @@ def test_k_fragment_reads_conflict_free(dp):
             assert len(set(slots)) == 16
 
 
+def cm_tile(dp, gb):
+    """LDS byte -> (key, byte of the key's row) after dma_tile_cm<DPW, gb> has moved one
+    64-key tile with contiguous rows (rowb = 2 dp): wave wv, block r, lane l."""
+    rowb, dpw = 2 * dp, (64 * (dp // 8)) // 256
+    kpb = 1024 // gb
+    bpg = 64 // kpb
+    lds = {}
+    for wv in range(4):
+        k0 = (wv % bpg) * kpb
+        for r in range(dpw):
+            assert 64 * r + gb <= rowb                     # soffset + group width within a row
+            base = k0 * rowb + (wv // bpg) * gb + 64 * r
+            for lane in range(64):
+                if gb == 32:
+                    doff = (lane >> 1) * rowb + (((lane & 1) ^ ((lane >> 4) & 1)) << 4)
+                else:
+                    doff = (lane >> 2) * rowb + ((lane & 3) << 4)
+                key, byte = divmod(base + doff, rowb)
+                assert byte + 16 <= rowb
+                dst = wv * 1024 + r * 4096 + lane * 16
+                for x in range(16):
+                    assert dst + x not in lds
+                    lds[dst + x] = (key, byte + x)
+    assert sorted(lds) == list(range(64 * rowb))
+    return lds
+
+
 @pytest.mark.parametrize("dp", [64, 128])
-def test_v_transposing_reads_conflict_free(dp):
-    # half-wave of ds_read_b64_tr_b16: lanes r in 0..15 of groups g in {0,1}, 8 B each
-    rowb = dp * 2
-    for kc0 in range(0, 64, 16):
-        for h in (0, 1):
-            for dt in range(dp // 32):
-                slots = set()
-                for g in (0, 1):
-                    for r in range(16):
-                        k = kc0 + 4 * h + (r >> 2)
-                        d = 32 * dt + 16 * g + 4 * (r & 3)
-                        addr = k * rowb + (((d >> 3) ^ swz(dp, k)) << 4) + ((d >> 2) & 1) * 8
-                        slots.add((addr % 256) // 8)
-                assert len(slots) == 32
+def test_cm_k_fragments(dp):
+    lds = cm_tile(dp, 32)
+    for s in range(2):
+        for c in range(dp // 16):
+            phases = {}
+            for lane in range(64):
+                l32, hh = lane & 31, lane >> 5
+                a = c * 2048 + s * 1024 + l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4)
+                assert [lds[a + x] for x in range(16)] == [(32 * s + l32, (2 * c + hh) * 16 + x) for x in range(16)]
+                phases.setdefault(lane // 16, []).extend((a // 4 + i) % 64 for i in range(4))
+            assert all(len(set(b)) == 64 for b in phases.values())
+
+
+@pytest.mark.parametrize("dp", [64, 128])
+def test_cm_v_transposing_reads(dp):
+    lds = cm_tile(dp, 64)
+    for dt in range(dp // 32):
+        for c4 in range(4):
+            for half in range(2):
+                phases = {}
+                for lane in range(64):
+                    r, g, hh = lane & 15, lane >> 4, lane >> 5
+                    a = dt * 4096 + c4 * 1024 + half * 512 + (4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3)
+                    key = 16 * c4 + 8 * half + 4 * hh + (r >> 2)
+                    d = 32 * dt + 16 * (g & 1) + 4 * (r & 3)
+                    assert [lds[a + x] for x in range(8)] == [(key, 2 * d + x) for x in range(8)]
+                    phases.setdefault(lane // 32, []).extend((a // 4 + i) % 64 for i in range(2))
+                assert all(len(set(b)) == 64 for b in phases.values())
