@@ -62,18 +62,6 @@ struct FastTile {
   static constexpr int NDT = DP / 32;            // 32-channel tiles of O^T
 };
 
-// Row-major K tiles (replay_fast_kernel): XOR applied to the 16-byte chunk index of row
-// `key` so that a K fragment read (16 consecutive keys, one logical chunk per access phase;
-// 64 banks x 4 B = 256 B per cycle) hits 16 distinct chunks: the key's two low bits move
-// into the chunk's high bits. For 128-byte rows (D = 64) two rows share a bank cycle, so
-// key bit 0 selects the half and bits 1..3 are spread the same way. Only key bits 0..3
-// matter, so the swizzle of key k and of k + 16j agree and every per-lane LDS offset is
-// fixed for the whole kernel.
-template <int DP>
-__device__ __forceinline__ int swz(int key) {
-  return DP == 128 ? (((key & 3) << 2) | ((key >> 2) & 3)) : ((((key >> 1) & 1) << 2) | ((key >> 2) & 3));
-}
-
 // IEEE maximum (v_maximum3_f32): the operands are MFMA results or -inf, so the NaN-quieting
 // canonicalisation that fmaxf implies is not needed.
 __device__ __forceinline__ float vmax(float x, float y) { return __builtin_elementwise_maximum(x, y); }
@@ -114,19 +102,6 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + r * 4096), 16, doff, 64 * r, 0, 0);
 }
 
-// The same DMA with one offset register per block (replay_fast_kernel): the tile's first row
-// enters through the buffer base and the record count ends at row N, so rows past N read as
-// zero.
-template <int DPW>
-__device__ __forceinline__ void dma_tile(const unsigned char* g, u32 rowb, const u32* doff, int kb, int N,
-                                         unsigned char* ldst, int wv) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g + (size_t)kb * rowb), (short)0, (int)((u32)(N - kb) * rowb), 0x00020000);
-#pragma unroll
-  for (int r = 0; r < DPW; ++r)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(ldst + (r * 4 + wv) * 1024), 16, doff[r], 0, 0, 0);
-}
-
 // NW waves of one row tile each (8: two waves per SIMD; 12: three, for the attention-only
 // variant at D = 128, which then reads K fragments in two halves and V fragments without
 // prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
@@ -134,7 +109,7 @@ __device__ __forceinline__ void dma_tile(const unsigned char* g, u32 rowb, const
 template <typename E, int DP, int NW, bool FUSED>
 __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
-  constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
+  constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
   constexpr int KH = NW > 8 ? 2 : 1;             // K fragment reads per 32-key half
   static_assert(NW % 2 == 0 && NW >= 4, "row tiles per workgroup");
@@ -511,14 +486,15 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 // (the value L1 norm is applied afterwards, as in the fused schedule). Without O, P and V
 // this traversal needs far fewer registers than traversal 1. A workgroup holds 8 row tiles
 // that share every K tile (one FP32 atomic per key and tile per workgroup), as 8/TPW waves
-// of TPW row tiles each. TPW = 1 runs at four waves per SIMD; TPW = 2 (the default) at two,
-// with every K fragment read from LDS feeding two MFMAs: that halves the LDS read traffic,
-// the co-bottleneck of this traversal next to the MFMAs, and measures about 3% faster. (At
-// three waves per SIMD, TPW = 2 does not fit the 168-register budget without spills.)
+// of TPW row tiles each. TPW = 1 runs at four waves per SIMD. TPW = 2 (the default) runs at
+// three (three workgroups per CU; 168 registers with a few values spilled, 1.5% faster than
+// at two), with every K fragment read from LDS feeding two MFMAs: that halves the LDS read
+// traffic, the co-bottleneck of this traversal next to the MFMAs, and measures about 3%
+// faster than TPW = 1. The K tiles use the attention kernel's channel-group-major layout.
 template <typename E, int DP, int TPW>
-__global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
-  constexpr int BN = T::BN, NDC = T::NDC, ROWB = T::ROWB, TILE = T::TILE, CPR = T::CPR;
+  constexpr int BN = T::BN, NDC = T::NDC, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
   constexpr int NW = 8 / TPW;                    // waves per workgroup
   constexpr float NEG_INF = -__builtin_huge_valf();
@@ -577,22 +553,11 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
     for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
   }
 
-  // fixed per-lane K fragment offsets; the empty asm keeps them in registers (the compiler
-  // would otherwise recompute them in every tile, about 25 vector instructions)
-  u32 koff[NDC];
-#pragma unroll
-  for (int c = 0; c < NDC; ++c) {
-    koff[c] = (u32)(l32 * ROWB + (((2 * c + hh) ^ swz<DP>(l32)) << 4));
-    asm volatile("" : "+v"(koff[c]));
-  }
+  // K tiles in the attention kernel's channel-group-major layout: fragment c of key
+  // 32s + l32 at c*2048 + s*1024 + koff; one DMA offset register (see dma_tile_cm)
+  const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
   const u32 krow = (u32)(a.ks[2] * 2);
-  u32 dk[DPW];
-#pragma unroll
-  for (int r = 0; r < DPW; ++r) {
-    const int c = (r * 4 + (wv & 3)) * 64 + lane;
-    const int key = c / CPR, pc = c % CPR;
-    dk[r] = (u32)key * krow + (u32)(pc ^ swz<DP>(key)) * 16u;
-  }
+  const u32 dk = (u32)(lane >> 1) * krow + (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
   const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
   float* imp_row = a.imp + (long long)bh * N;
 
@@ -612,7 +577,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
     if (dmaw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (it > it_lo) flush(kb - BN, BUF ^ 1);
-    if (dmaw && it + 1 < ntiles) dma_tile<DPW>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv);
+    if (dmaw && it + 1 < ntiles) dma_tile_cm<DPW, 32>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv);
     float cs[2] = {0.f, 0.f};
     if (kb <= wave_hi) {
       const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
@@ -623,7 +588,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
         for (int j = 0; j < TPW; ++j) sacc[j] = (f32x16){};
 #pragma unroll
         for (int c = 0; c < NDC; ++c) {
-          const u32x4 kf = *(const u32x4*)(kt + koff[c] + s * 32 * ROWB);
+          const u32x4 kf = *(const u32x4*)(kt + c * 2048 + s * 1024 + koff);
 #pragma unroll
           for (int j = 0; j < TPW; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
         }
@@ -657,7 +622,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 2) void replay_fast_kerne
     }
   };
 
-  if (dmaw) dma_tile<DPW>(kg, krow, dk, it_lo * BN, N, lds_k0, wv);
+  if (dmaw) dma_tile_cm<DPW, 32>(kg, krow, dk, it_lo * BN, N, lds_k0, wv);
   for (int it = it_lo; it < ntiles; it += 2) {
     step(it, 0);
     if (it + 1 < ntiles) step(it + 1, 1);

@@ -1,34 +1,10 @@
-"""Host-side check of the fast kernels' LDS layout rules (fe_attn_fast.hip), 64 banks x 4 B =
-256 B per cycle:
-* the row-major K tiles of replay_fast_kernel (`swz`): the chunk swizzle is a bijection per
-  row and a K fragment read phase touches distinct bank slots;
-* the channel-group-major K and V tiles of fused_fast_kernel (`dma_tile_cm`, `k_frags`,
-  `v_frag`): the DMA writes every LDS byte of a tile once, each fragment read returns the
-  key and channels the MFMA expects, and each read phase touches distinct bank slots."""
+"""Host-side check of the fast kernels' LDS tile layout (fe_attn_fast.hip `dma_tile_cm`,
+`k_frags`, `v_frag`, and the replay kernel's K reads): K and V tiles are stored
+channel-group-major. The DMA must write every LDS byte of a tile once, each fragment read
+must return the key and channels the MFMA expects, and each read phase must touch distinct
+bank slots (64 banks x 4 B = 256 B per cycle; 16 lanes per phase for 16-byte reads, 32 for
+8-byte transposing reads)."""
 import pytest
-
-
-def swz(dp, k):
-    if dp == 128:
-        return ((k & 3) << 2) | ((k >> 2) & 3)
-    return (((k >> 1) & 1) << 2) | ((k >> 2) & 3)
-
-
-@pytest.mark.parametrize("dp", [64, 128])
-def test_swizzle_is_bijective(dp):
-    cpr = dp // 8
-    for k in range(64):
-        assert sorted(c ^ swz(dp, k) for c in range(cpr)) == list(range(cpr))
-
-
-@pytest.mark.parametrize("dp", [64, 128])
-def test_k_fragment_reads_conflict_free(dp):
-    # 16 lanes of one phase: keys k0..k0+15, one logical chunk, 16 B each
-    rowb, cpr = dp * 2, dp // 8
-    for k0 in range(0, 64, 16):
-        for lc in range(cpr):
-            slots = [((k * rowb + ((lc ^ swz(dp, k)) << 4)) % 256) // 16 for k in range(k0, k0 + 16)]
-            assert len(set(slots)) == 16
 
 
 def cm_tile(dp, gb):
