@@ -3,9 +3,8 @@
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
 //
 //   * A workgroup is NW waves of one 32-query row tile each, all on one KV head (GQA
-//     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. The
-//     attention-only kernel at D = 128 runs 12 waves, three per SIMD; the kernel with the
-//     fused replay traversal, and D = 64, run 8.
+//     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. At
+//     D = 128 the kernels run 12 waves, three per SIMD; at D = 64, 8 (two workgroups per CU).
 //   * The K/V buffers hold pairs of 64-key tiles: one barrier per 128 keys.
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
@@ -102,9 +101,8 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + r * 4096), 16, doff, 64 * r, 0, 0);
 }
 
-// NW waves of one row tile each (8: two waves per SIMD; 12: three, for the attention-only
-// variant at D = 128, which then reads K fragments in two halves and V fragments without
-// prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
+// NW waves of one row tile each (8: two waves per SIMD; 12: three, at D = 128, which then
+// reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
 template <typename E, int DP, int NW, bool FUSED>
 __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(const AttnArgs a) {
@@ -427,13 +425,18 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
         f32x16 sacc[2];
   #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          u32x4 kf[NDC];
-          k_frags(BUF, 0, s, 0, kf);
-          FE_PRIO_HI();
-          sacc[s] = E::mfma(qf[0], kf[0], (f32x16){});
   #pragma unroll
-          for (int c = 1; c < NDC; ++c) sacc[s] = E::mfma(qf[c], kf[c], sacc[s]);
-          FE_PRIO_LO();
+          for (int h = 0; h < KH; ++h) {
+            u32x4 kf[NDC / KH];
+            k_frags(BUF, 0, s, h, kf);
+            FE_PRIO_HI();
+  #pragma unroll
+            for (int c = 0; c < NDC / KH; ++c) {
+              const int cc = h * (NDC / KH) + c;
+              sacc[s] = cc == 0 ? E::mfma(qf[0], kf[c], (f32x16){}) : E::mfma(qf[cc], kf[c], sacc[s]);
+            }
+            FE_PRIO_LO();
+          }
         }
         if (a.causal && kb + BN - 1 > q0) {
   #pragma unroll
@@ -654,18 +657,18 @@ FusedPlan fast_entry(const char* name) {
 }
 
 // Per (dtype, D): the attention-only kernel (split schedule, or no importance) and the fused
-// kernel with the replay traversal (fe_prefill without a workspace). At D = 64 the
-// attention-only kernel stays at 8 waves: 125 registers and 68 KiB of LDS already put two
-// workgroups, four waves per SIMD, on a CU.
+// kernel with the replay traversal (fe_prefill without a workspace). At D = 64 both stay at
+// 8 waves: about 115 registers and 68 KiB of LDS already put two workgroups, four waves per
+// SIMD, on a CU.
 FusedPlan g_fast[] = {
     fast_entry<F16, 64, 8, false>("attn_fast<f16,64>"),
     fast_entry<F16, 64, 8, true>("fused_fast<f16,64>"),
     fast_entry<F16, 128, 12, false>("attn_fast<f16,128>"),
-    fast_entry<F16, 128, 8, true>("fused_fast<f16,128>"),
+    fast_entry<F16, 128, 12, true>("fused_fast<f16,128>"),
     fast_entry<BF16, 64, 8, false>("attn_fast<bf16,64>"),
     fast_entry<BF16, 64, 8, true>("fused_fast<bf16,64>"),
     fast_entry<BF16, 128, 12, false>("attn_fast<bf16,128>"),
-    fast_entry<BF16, 128, 8, true>("fused_fast<bf16,128>"),
+    fast_entry<BF16, 128, 12, true>("fused_fast<bf16,128>"),
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

@@ -116,8 +116,9 @@ def test_kernel_resources():
     assert "fused_fast<bf16,128>" in names and "select_rows" in names
     fast = [r for r in res if r["kernel"] == "fused_fast<bf16,128>"][0]
     # K/V double buffers of two 64-key tiles (8 x 64 rows x 256 B) plus the column-sum
-    # exchange of the eight waves, all static LDS
-    assert 0 < fast["registers_per_thread"] <= 256 and fast["lds_static_bytes"] == 8 * 64 * 256 + 2 * 8 * 64 * 4
+    # exchange of the twelve waves, all static LDS; three waves per SIMD
+    assert 0 < fast["registers_per_thread"] <= 168 and fast["lds_static_bytes"] == 8 * 64 * 256 + 2 * 12 * 64 * 4
+    assert fast["max_threads_per_block"] >= 768
     # the attention-only kernel of the split schedule: 12 waves, three per SIMD
     attn = [r for r in res if r["kernel"] == "attn_fast<bf16,128>"][0]
     assert 0 < attn["registers_per_thread"] <= 168 and 8 * 64 * 256 <= attn["lds_static_bytes"] <= 8 * 64 * 256 + 64
