@@ -18,8 +18,9 @@
 //     the waitcount pass can see that the DMA into one buffer does not alias reads of the
 //     other (reads of tiles t, t+1 never wait for the DMA of t+2, t+3).
 //   * The A operand of O^T = V^T P^T (eight keys of one channel per lane) comes straight
-//     from the row-major V tile with two ds_read_b64_tr_b16 transposing reads; the key
-//     order of the read matches the S^T accumulator row order that becomes P^T.
+//     from the V tile (rows of one 32-channel tile) with two ds_read_b64_tr_b16 transposing
+//     reads; the key order of the read matches the S^T accumulator row order that becomes
+//     P^T.
 //   * Row maxima use v_maximum3_f32 (no NaN canonicalisation); O is rescaled only when
 //     some row's running max actually rises (wave vote).
 //   * Masked logits are set to -inf in place, so masking costs one compare/select per
