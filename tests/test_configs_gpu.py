@@ -61,6 +61,30 @@ def test_edge_noncausal_noncontiguous_extreme_zero_rows():
     assert_same_selection(~evicted, torch.from_numpy(ref_keep), ref_imp.cpu(), budget, atol=1e-2, rtol=1e-3)
 
 
+def test_edge_and_llama_configs_through_workspace_free_entry_point():
+    """The same two configs through fe_prefill (the single fused kernel, no workspace)."""
+    from test_schedules_gpu import _run
+    print("config edge + llama8k, fe_prefill", flush=True)
+    b, n, hq, hk, d = 2, 4000, 8, 2, 128
+    q = seeded_randn((b, n, hq, d), torch.float16, 20260910, scale=30).transpose(1, 2)
+    k = seeded_randn((b, n, hk, d), torch.float16, 20260911, scale=30).transpose(1, 2)
+    v = seeded_randn((b, n, hk, d), torch.float16, 20260912).transpose(1, 2).clone()
+    v[:, :, torch.randperm(n, generator=torch.Generator().manual_seed(5))[: n // 10].cuda()] = 0
+    v = v.transpose(1, 2).contiguous().transpose(1, 2)
+    out, imp = _run(q, k, v, False, False, 0.0, 0, use_ws=False)
+    ref_out, ref_imp = chunked(q.float(), k.float(), v.float(), causal=False, value_weighted=False, block=512)
+    assert (out.float() - ref_out).abs().max() <= 5e-3
+    assert rel_err(imp, ref_imp) <= 1e-3
+
+    n, hq, hk = 8192, 32, 8
+    q, k = _outlier_qk(n, hq, hk, d, 20260910)
+    v = seeded_randn((1, hk, n, d), torch.bfloat16, 20260913)
+    out, imp = _run(q, k, v, True, True, 0.1, 0, use_ws=False)
+    ref_out, ref_imp = chunked(q, k, v, block=1024, recency_decay=0.1)
+    assert (out.float() - ref_out).abs().max() <= 2e-2
+    assert rel_err(imp, ref_imp) <= 1e-3
+
+
 def _outlier_qk(n, hq, hk, d, seed):
     q = torch.randn((1, hq, n, d), generator=torch.Generator().manual_seed(seed))
     k = torch.randn((1, hk, n, d), generator=torch.Generator().manual_seed(seed + 1))
