@@ -1,24 +1,30 @@
 """Benchmark of the flash_evict prefill hot path on one MI355X.
 
-A step is one full `evict()` layer (zero-init, fused attention + replay-score kernel,
-value-norm scaling, radix top-k + mask) over resident synthetic bf16 inputs at the
-headline shape B=1, Hq=32, Hkv=8, N=32768, D=128, causal, budget 1024, recency_decay 0.1,
-reserved_recent 64, all-query replay (observation_window 0).
+A step is one full `evict()` layer (zero-init, attention kernel + replay kernel, value-norm
+scaling, radix top-k + mask) over resident synthetic bf16 inputs at the headline shape B=1,
+Hq=32, Hkv=8, N=32768, D=128, causal, budget 1024, recency_decay 0.1, reserved_recent 64,
+all-query window (observation_window 0).
+
+Work counts. The metric's definition of a layer's work is 4*D*P_attn + 2*D*P_replay with
+P_attn = B*Hq*N(N+1)/2 (causal) and P_replay the query-key pairs of the last W query rows
+(W = the observation window, all rows when 0): 13.19 TFLOP at the headline. The library
+replays only the last R = fe_replay_rows(N, W, recency_decay) of them, because rows whose
+recency weight exp(-decay*(N-1-q)) is exactly zero in FP32 (decay*(N-1-q) >= 105) add exactly
+nothing to the importance: 9.07 TFLOP executed at the headline (R = 1050).
 
 Prints one JSON line on stdout:
-  value        = the layer's algorithmic attention+score TFLOP / measured layer time
-  ms_per_step  = ms per layer (the metric's first half)
-  roofline     = the fused kernel alone: the TFLOP it executes / its mean duration, timed
-                 with HIP events recorded by the library on the kernel's own stream
-  cpu_baseline = the CPU oracle (oracle/attention.chunked) on one query head of the same
-                 workload, extrapolated to the layer (reported only)
-Algorithmic work of a layer (the metric's definition): 4*D*P_attn + 2*D*P_replay with
-P_attn = B*Hq*N(N+1)/2 (causal) and P_replay the query-key pairs of the last W query rows
-(W = the observation window, all rows when 0). The library replays only the last
-R = fe_replay_rows(N, W, recency_decay) of them: rows whose recency weight
-exp(-decay*(N-1-q)) is exactly zero in FP32 (decay*(N-1-q) >= 105) add exactly nothing to the
-importance. The roofline counts the work executed (R rows), so its fraction of peak is the
-MFMA utilisation; `config` lists both counts.
+  value              = TFLOP the kernels execute per layer / measured layer time
+  value_defined_work = the metric's defined TFLOP per layer / measured layer time
+  ms_per_step        = ms per layer (the metric's first half)
+  roofline           = the attention + replay kernels alone: executed TFLOP / their mean
+                       duration, timed with HIP events the library records on the kernels'
+                       own stream; frac = fraction of dense bf16 MFMA peak
+  full_replay        = the same inputs with recency_decay 0 (every one of the 32768 rows
+                       replayed, so executed = defined work): layer ms and the attention +
+                       replay kernels' ms, TFLOP/s and fraction of peak, from the same run
+  cpu_baseline       = the CPU oracle (oracle/attention.chunked, FP32 torch) on a sample of
+                       the same workload's query heads, on the box's usable host cores
+                       (reported only)
 """
 import argparse
 import json
@@ -71,14 +77,46 @@ def algorithmic_flop(b, hq, n, d, window, recency_decay=0.0, causal=True, effect
     return 4 * d * p_attn + 2 * d * p_replay
 
 
-def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
-    """Time the CPU oracle on `sample_heads` query heads (all N queries, their KV heads) and
-    extrapolate to the layer; also time the library's host selection on the layer's scores."""
-    import ctypes
+def _usable_cores():
+    """Host cores this process may use: its affinity set, capped by a cgroup CPU quota when
+    one is set (containers often pin many cores but grant a smaller share)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        quota = None
+    cores = affinity if quota is None else max(1, min(affinity, int(quota + 0.999)))
+    return cores, affinity, quota
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(q, k, v, kw, executed_flop, sample_heads=8):
+    """The reference's CPU-capable path restated (oracle/attention.chunked: FP32 softmax
+    attention and importance, then the library's host selection) on the host cores.
+
+    Times `sample_heads` query heads over all N queries after one untimed warm-up, and
+    reports the rate on the same work count as the GPU line's `value` (the per-head work is
+    uniform, so the sample's rate is the layer's rate); ms_per_layer scales the sample time
+    by the head count."""
     import torch
     from oracle.attention import chunked
     from flash_evict import _lib
-    torch.set_num_threads(threads)
+    cores, affinity, quota = _usable_cores()
+    torch.set_num_threads(cores)
     b, hq, n, d = q.shape
     hk = k.shape[1]
     g = hq // hk
@@ -87,12 +125,12 @@ def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
     qc, kc, vc = q[:1, :sample_heads].cpu(), k[:1, :kv_needed].cpu(), v[:1, :kv_needed].cpu()
     args = dict(causal=True, value_weighted=True, recency_decay=kw["recency_decay"],
                 observation_window=kw["observation_window"], block=1024)
+    chunked(qc, kc, vc, heads=[(0, 0)], query_rows=[(0, 2048)], **args)        # warm-up
     t0 = time.perf_counter()
     _, imp = chunked(qc, kc, vc, **args)
     dt = time.perf_counter() - t0
     layer_s = dt * (b * hq) / sample_heads
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
-    # host selection (fe_select_host) on a [B*Hkv, N] score array of the layer's size
+    # host selection (fe_select_host, one thread) on a [B*Hkv, N] score array of the layer's size
     scores = imp[0, :1].expand(b * hk, n).contiguous()
     idx = torch.empty((b * hk, kw["budget"]), dtype=torch.int64)
     mask = torch.empty((b * hk, n), dtype=torch.bool)
@@ -101,27 +139,49 @@ def cpu_baseline(q, k, v, kw, threads, sample_heads=8):
     _lib.check(L.fe_select_host(scores.data_ptr(), b * hk, n, n, kw["budget"], kw["reserved_recent"],
                                 kw["pool_kernel"], idx.data_ptr(), mask.data_ptr(), 0), "fe_select_host")
     sel_ms = (time.perf_counter() - t1) * 1e3
-    cpu_model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
-        "value": round(flop / layer_s / 1e12, 4),
+        "value": round(executed_flop / layer_s / 1e12, 4),
         "unit": "TFLOP/s",
-        "ms_per_layer": round(layer_s * 1e3 + sel_ms, 1),
-        "cores": threads,
+        "cores": cores,
         "kind": "port",
+        "sample": "oracle chunked FP32, %d of %d q-heads x %d rows, %.1f s" % (sample_heads, b * hq, n, dt),
+        "ms_per_layer": round(layer_s * 1e3 + sel_ms, 1),
         "select_host_ms": round(sel_ms, 2),
-        "sample": "oracle/attention.chunked (FP32 torch CPU, 1024-query blocks) on %d of %d query heads "
-                  "(all %d queries), %.2f s measured, x%g extrapolated; selection: fe_select_host on "
-                  "%d x %d scores (1 thread); CPU %s" % (sample_heads, b * hq, n, dt, (b * hq) / sample_heads,
-                                                          b * hk, n, cpu_model),
+        "affinity_cores": affinity,
+        "cgroup_cpu_quota": quota,
+        "torch_threads": torch.get_num_threads(),
+        "cpu_model": _cpu_model(),
+        "note": "rate on the GPU line's executed-work count; ms_per_layer = sample time x %g + host selection "
+                "(1 thread); one untimed warm-up" % ((b * hq) / sample_heads),
     }
+
+
+def _timed_layers(step, steps, warmup, tag):
+    """Run `warmup` untimed and `steps` timed layers; return (ms per layer, fused-kernel ms
+    per launch, launches) with the fused kernels timed by the library's HIP events."""
+    import ctypes
+    import torch
+    from flash_evict import _lib
+    L = _lib.lib()
+    for i in range(warmup):
+        step()
+        torch.cuda.synchronize()
+        log("%s warmup %d/%d done" % (tag, i + 1, warmup))
+    _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
+    _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.check(L.fe_fused_timing_enable(0), "fe_fused_timing_enable")
+    launches = ctypes.c_int64(0)
+    fused_ms = ctypes.c_double(0.0)
+    _lib.check(L.fe_fused_timing_read(ctypes.byref(launches), ctypes.byref(fused_ms)), "fe_fused_timing_read")
+    ms = elapsed * 1e3 / steps
+    log("%s timed %d steps: %.3f ms/layer" % (tag, steps, ms))
+    return ms, fused_ms.value / max(1, launches.value), launches.value
 
 
 def main():
@@ -131,6 +191,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-full-replay", action="store_true")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "fused_attn_score_headline_traffic.json"),
                     help="rocprofv3 PMC summary giving HBM bytes per fused launch (optional)")
     args = ap.parse_args()
@@ -143,7 +204,6 @@ def main():
 
     import torch
     import flash_evict
-    from flash_evict import _lib
 
     b, hq, hk, n, d, kw = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
@@ -155,36 +215,29 @@ def main():
     v = torch.randn((b, hk, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
     torch.cuda.synchronize()
 
-    def step():
-        return flash_evict.evict(q, k, v, kw["budget"], reserved_recent=kw["reserved_recent"],
-                                 pool_kernel=kw["pool_kernel"], recency_decay=kw["recency_decay"],
-                                 observation_window=kw["observation_window"])
+    def make_step(decay):
+        def step():
+            return flash_evict.evict(q, k, v, kw["budget"], reserved_recent=kw["reserved_recent"],
+                                     pool_kernel=kw["pool_kernel"], recency_decay=decay,
+                                     observation_window=kw["observation_window"])
+        return step
 
     with torch.inference_mode():
-        for i in range(args.warmup):
-            step()
-            torch.cuda.synchronize()
-            log("warmup %d/%d done" % (i + 1, args.warmup))
-        L = _lib.lib()
-        _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
-        _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-        _lib.check(L.fe_fused_timing_enable(0), "fe_fused_timing_enable")
-        import ctypes
-        launches = ctypes.c_int64(0)
-        fused_ms = ctypes.c_double(0.0)
-        _lib.check(L.fe_fused_timing_read(ctypes.byref(launches), ctypes.byref(fused_ms)),
-                   "fe_fused_timing_read")
-    ms = elapsed * 1e3 / args.steps
-    log("timed %d steps: %.3f ms/layer" % (args.steps, ms))
+        ms, fused_avg_ms, launches = _timed_layers(make_step(kw["recency_decay"]), args.steps, args.warmup,
+                                                   "headline")
+        full = None
+        if kw["recency_decay"] > 0 and not args.no_full_replay:
+            fsteps = max(3, args.steps // 2)
+            f_ms, f_fused, f_launches = _timed_layers(make_step(0.0), fsteps, min(2, args.warmup), "full-replay")
+            f_flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], 0.0)
+            f_ach = f_flop / (f_fused * 1e-3) / 1e12
+            full = {"recency_decay": 0.0, "replay_rows": replay_rows(n, kw["observation_window"], 0.0),
+                    "executed_tflop": round(f_flop / 1e12, 4), "ms_per_layer": round(f_ms, 4),
+                    "fused_mean_ms": round(f_fused, 4), "fused_achieved_tflops": round(f_ach, 2),
+                    "fused_frac": round(f_ach / PEAK_BF16_TFLOPS, 4), "launches": f_launches,
+                    "steps": fsteps}
     flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
     executed = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
-    fused_avg_ms = fused_ms.value / max(1, launches.value)
     achieved = executed / (fused_avg_ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(args.traffic_json):
@@ -197,7 +250,7 @@ def main():
             traffic = None
     record = {
         "metric": "ms/layer + fused attn+score TFLOP/s (% MFMA peak), N=32K Hq32/Hkv8 D128 bf16",
-        "value": round(flop / (ms * 1e-3) / 1e12, 2),
+        "value": round(executed / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -212,15 +265,16 @@ def main():
                    "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4),
                    "replay_rows": replay_rows(n, kw["observation_window"], kw["recency_decay"]),
                    "executed_tflop": round(executed / 1e12, 4)},
+        "value_defined_work": round(flop / (ms * 1e-3) / 1e12, 2),
         "roofline": {"bound": "mfma", "kernel": "fused_attn_score", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches.value},
+                     "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches},
         "fused_share_of_layer": round(fused_avg_ms / ms, 4),
+        "full_replay": full,
     }
     if not args.no_cpu_baseline:
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        log("cpu baseline on %d threads ..." % threads)
-        record["cpu_baseline"] = cpu_baseline(q, k, v, kw, threads)
+        log("cpu baseline ...")
+        record["cpu_baseline"] = cpu_baseline(q, k, v, kw, executed)
     else:
         record["cpu_baseline"] = None
     print(json.dumps(record), flush=True)

@@ -6,7 +6,6 @@
 #include <string.h>
 
 #include <algorithm>
-#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -22,9 +21,15 @@ int check_select_args(const float* scores, int64_t rows, int64_t n, int64_t row_
 namespace {
 thread_local std::string g_error;
 
-std::mutex g_timing_mutex;
-bool g_timing_on = false;
-std::vector<std::pair<hipEvent_t, hipEvent_t>> g_timing_events;
+// Fused-kernel timing is per calling thread: a thread that enables it times only its own
+// fe_prefill calls, and reads back only its own events. (No destructor: event pairs still
+// unread when a thread exits are left to the runtime's teardown rather than destroyed from
+// a thread-exit hook that may run after it.)
+struct TimingState {
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+};
+thread_local TimingState g_timing;
 
 // Same order map as the device kernels: larger float <=> larger key, -0 == +0, NaN on top.
 inline uint32_t order_key(float f) {
@@ -39,15 +44,9 @@ inline uint32_t order_key(float f) {
 void set_error(const std::string& msg) { g_error = msg; }
 void clear_error() { g_error.clear(); }
 
-bool fused_timing_enabled() {
-  std::lock_guard<std::mutex> lock(g_timing_mutex);
-  return g_timing_on;
-}
+bool fused_timing_enabled() { return g_timing.on; }
 
-void fused_timing_push(hipEvent_t start, hipEvent_t stop) {
-  std::lock_guard<std::mutex> lock(g_timing_mutex);
-  g_timing_events.emplace_back(start, stop);
-}
+void fused_timing_push(hipEvent_t start, hipEvent_t stop) { g_timing.events.emplace_back(start, stop); }
 
 }  // namespace fe
 
@@ -59,18 +58,14 @@ extern "C" int fe_abi_version(void) { return 1; }
 
 extern "C" int fe_fused_timing_enable(int enable) {
   clear_error();
-  std::lock_guard<std::mutex> lock(g_timing_mutex);
-  g_timing_on = enable != 0;
+  g_timing.on = enable != 0;
   return FE_OK;
 }
 
 extern "C" int fe_fused_timing_read(int64_t* launches, double* total_ms) {
   clear_error();
   std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
-  {
-    std::lock_guard<std::mutex> lock(g_timing_mutex);
-    ev.swap(g_timing_events);
-  }
+  ev.swap(g_timing.events);
   double total = 0.0;
   int rc = FE_OK;
   for (auto& p : ev) {

@@ -33,7 +33,6 @@
 //     different KV heads (the hardware deals blocks round-robin over the 8 XCDs, so each
 //     XCD's L2 sees a small set of KV heads).
 #include <math.h>
-#include <mutex>
 #include <string>
 #include <vector>
 
@@ -501,9 +500,6 @@ std::vector<FusedEntry>& fused_table() {
   return t;
 }
 
-std::mutex g_attr_mutex;
-std::vector<const void*> g_attr_done;
-
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int vec_ok(const void* p, const int64_t* st, int64_t D) {
@@ -512,12 +508,20 @@ int vec_ok(const void* p, const int64_t* st, int64_t D) {
 
 }  // namespace
 
+// The generic kernels take their LDS dynamically (up to 143 KiB at DP = 256), above the
+// default dynamic limit: raise it for every kernel of the table, once per process, on first
+// use (a function-local static, so the initialisation is thread-safe and nothing is mutated
+// afterwards). The fast kernels use static LDS only and need nothing.
 hipError_t prepare_plan(const FusedPlan& plan) {
-  std::lock_guard<std::mutex> lock(g_attr_mutex);
-  for (const void* f : g_attr_done)
-    if (f == plan.fn) return hipSuccess;
-  hipError_t err = hipFuncSetAttribute(plan.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);
-  if (err == hipSuccess) g_attr_done.push_back(plan.fn);
+  if (plan.lds == 0) return hipSuccess;
+  static const hipError_t err = [] {
+    for (const auto& e : fused_table()) {
+      const hipError_t r =
+          hipFuncSetAttribute((const void*)e.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)e.lds);
+      if (r != hipSuccess) return r;
+    }
+    return hipSuccess;
+  }();
   return err;
 }
 
@@ -674,11 +678,20 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       return FE_ERR_HIP;
     }
   }
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // Optional timing of the attention (+ replay) kernels on the caller's stream: the event
+  // pair goes to the calling thread's record once both events are recorded, and is
+  // destroyed on every earlier return.
+  struct EventPair {
+    hipEvent_t e[2] = {nullptr, nullptr};
+    ~EventPair() {
+      for (hipEvent_t x : e)
+        if (x) (void)hipEventDestroy(x);
+    }
+  } ev;
   const bool timed = fused_timing_enabled();
   if (timed) {
-    if (hipEventCreate(&ev0) != hipSuccess || hipEventCreate(&ev1) != hipSuccess ||
-        hipEventRecord(ev0, stream) != hipSuccess) {
+    if (hipEventCreate(&ev.e[0]) != hipSuccess || hipEventCreate(&ev.e[1]) != hipSuccess ||
+        hipEventRecord(ev.e[0], stream) != hipSuccess) {
       set_error("fe_prefill: timing event setup failed");
       return FE_ERR_HIP;
     }
@@ -711,11 +724,12 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     }
   }
   if (timed) {
-    if (hipEventRecord(ev1, stream) != hipSuccess) {
+    if (hipEventRecord(ev.e[1], stream) != hipSuccess) {
       set_error("fe_prefill: timing event record failed");
       return FE_ERR_HIP;
     }
-    fused_timing_push(ev0, ev1);
+    fused_timing_push(ev.e[0], ev.e[1]);
+    ev.e[0] = ev.e[1] = nullptr;
   }
   if (score && value_weighted) {
     const long long rows = B * Hkv * N;

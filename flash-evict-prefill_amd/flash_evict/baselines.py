@@ -17,8 +17,13 @@ from .prefill import _DTYPES, _select
 
 
 def flash_attention(q, k, v):
-    """Causal GQA attention through torch's fused SDPA kernels (baselines.py:7-9)."""
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+    """Causal GQA attention through torch's flash SDPA kernel alone (baselines.py:7-9).
+
+    Only SDPBackend.FLASH_ATTENTION is admitted, as in the reference, so the comparison
+    kernel is pinned: a shape that backend rejects raises torch's error instead of running
+    on another backend.
+    """
+    with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
         return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
 
 

@@ -153,10 +153,13 @@ int fe_snap_scores(const void* q, const void* k, float* scores, int64_t B, int64
                    void* hip_stream);
 
 /*
- * Timing of the fused attention+score kernel alone: when enabled, fe_prefill records a
- * HIP event pair around that kernel on the caller's stream. fe_fused_timing_read waits
- * for the recorded events, returns the number of timed launches and their total
- * duration in milliseconds, and clears the record.
+ * Timing of the attention + importance kernels alone (the fused kernel, or the attention
+ * and replay kernels of the split schedule): when enabled, fe_prefill / fe_prefill_ws
+ * record a HIP event pair around them on the caller's stream. The switch and the record
+ * are per calling thread: a thread times only its own calls and reads only its own
+ * events. fe_fused_timing_read waits for the recorded events (not for the stream),
+ * returns the number of timed launches and their total duration in milliseconds, and
+ * clears the thread's record. No counterpart in the reference (benchmark support).
  */
 int fe_fused_timing_enable(int enable);
 int fe_fused_timing_read(int64_t* launches, double* total_ms);

@@ -41,3 +41,38 @@ def assert_same_selection(keep, ref_keep, ref_scores, budget, recent=0, atol=0.0
         near = (past[diff] - thr).abs() <= atol + rtol * thr.abs()
         assert bool(near.all()), ("selection differs beyond near-ties", r, diff.tolist(),
                                   past[diff].tolist(), float(thr))
+
+
+def assert_importance_close(imp, ref, rtol=1e-3, floor=1e-30):
+    """Element-wise importance bound: |imp - ref| <= rtol * |ref| + floor for every key.
+
+    Unlike a bound normalised by the row maximum, this binds on every key, including the
+    many whose importance lies orders of magnitude below the largest. Returns the largest
+    relative error over the elements above the floor (for the log)."""
+    imp = imp.detach().double()
+    ref = ref.detach().to(imp.device).double()
+    assert imp.shape == ref.shape, (imp.shape, ref.shape)
+    err = (imp - ref).abs()
+    bound = rtol * ref.abs() + floor
+    bad = err > bound
+    if bool(bad.any()):
+        i = int(bad.flatten().nonzero()[0])
+        raise AssertionError("importance differs beyond %g*|ref| + %g at %d of %d elements; first at flat index %d: "
+                             "kernel %r, oracle %r" % (rtol, floor, int(bad.sum()), bad.numel(), i,
+                                                       float(imp.flatten()[i]), float(ref.flatten()[i])))
+    big = ref.abs() > floor
+    return float((err[big] / ref.abs()[big]).max()) if bool(big.any()) else 0.0
+
+
+def out_err_all_rows(out, q, k, v, block=2048, **kw):
+    """Max-abs error of the attention output against the FP32 oracle over every row of every
+    query head, computed one head at a time (oracle.attention.chunked on out's device)."""
+    from oracle.attention import chunked
+    b, hq = out.shape[:2]
+    worst = 0.0
+    for bi in range(b):
+        for h in range(hq):
+            ref_out, _ = chunked(q, k, v, heads=[(bi, h)], block=block, value_weighted=False, **kw)
+            worst = max(worst, float((out[bi, h].float() - ref_out[bi, h]).abs().max()))
+            del ref_out
+    return worst

@@ -1,9 +1,13 @@
 """GPU parity on the five workload configurations of the project brief.
 
 Tolerances (stated per config): attention output max-abs-err <= 2e-2 (bf16) / 5e-3 (fp16);
-importance relative error <= 1e-3 (atomic reordering); selected index sets identical except
-for near-ties within that tolerance. The oracle runs in FP32 -- on the CPU for the small
-configs, and (same code, oracle/attention.chunked) on the GPU in float32 for the large ones.
+importance element-wise |kernel - oracle| <= 1e-3 * |oracle| + floor, for every key (atomic
+reordering); selected index sets identical except for near-ties within that tolerance. The
+floor is 1e-30 (below any importance these inputs produce) except for the edge config, whose
+x30 logits make the FP32 logits themselves uncertain in the last bits: there it is 1e-6 in
+units of one query row's probability mass (H2O mass, every row sums to 1). The oracle runs
+in FP32 -- on the CPU for the small configs, and (same code, oracle/attention.chunked) on the
+GPU in float32 for the large ones.
 """
 import math
 
@@ -13,13 +17,11 @@ import torch
 import flash_evict
 from oracle.attention import chunked, materialized
 from oracle import select as osel
-from _helpers import assert_same_selection, seeded_randn
+from _helpers import assert_importance_close, assert_same_selection, out_err_all_rows, seeded_randn
 
 pytestmark = pytest.mark.gpu
 
-
-def rel_err(a, b):
-    return float((a.double() - b.double()).abs().max() / b.double().abs().max().clamp_min(1e-30))
+EDGE_FLOOR = 1e-6      # x30 logits: FP32 logit rounding bounds the attainable accuracy of tiny masses
 
 
 def test_tiny_fp16_dense():
@@ -56,7 +58,8 @@ def test_edge_noncausal_noncontiguous_extreme_zero_rows():
     ref_out, ref_imp = chunked(q.float(), k.float(), v.float(), causal=False, value_weighted=False, block=512)
     assert torch.isfinite(out).all() and torch.isfinite(imp).all()
     assert (out.float() - ref_out).abs().max() <= 5e-3
-    assert rel_err(imp, ref_imp) <= 1e-3
+    rel = assert_importance_close(imp, ref_imp, rtol=1e-3, floor=EDGE_FLOOR)
+    print("edge importance element-wise max rel err %.3e" % rel, flush=True)
     _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), budget)
     assert_same_selection(~evicted, torch.from_numpy(ref_keep), ref_imp.cpu(), budget, atol=1e-2, rtol=1e-3)
 
@@ -74,7 +77,7 @@ def test_edge_and_llama_configs_through_workspace_free_entry_point():
     out, imp = _run(q, k, v, False, False, 0.0, 0, use_ws=False)
     ref_out, ref_imp = chunked(q.float(), k.float(), v.float(), causal=False, value_weighted=False, block=512)
     assert (out.float() - ref_out).abs().max() <= 5e-3
-    assert rel_err(imp, ref_imp) <= 1e-3
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=EDGE_FLOOR)
 
     n, hq, hk = 8192, 32, 8
     q, k = _outlier_qk(n, hq, hk, d, 20260910)
@@ -82,7 +85,7 @@ def test_edge_and_llama_configs_through_workspace_free_entry_point():
     out, imp = _run(q, k, v, True, True, 0.1, 0, use_ws=False)
     ref_out, ref_imp = chunked(q, k, v, block=1024, recency_decay=0.1)
     assert (out.float() - ref_out).abs().max() <= 2e-2
-    assert rel_err(imp, ref_imp) <= 1e-3
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
 
 
 def _outlier_qk(n, hq, hk, d, seed):
@@ -103,7 +106,8 @@ def test_llama_8k_outliers():
     out, imp, idx, evicted = flash_evict.evict(q, k, v, 1024, reserved_recent=64, **kw)
     ref_out, ref_imp = chunked(q, k, v, block=1024, **kw)          # FP32 on the GPU
     assert (out.float() - ref_out).abs().max() <= 2e-2
-    assert rel_err(imp, ref_imp) <= 1e-3
+    rel = assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    print("llama8k importance element-wise max rel err %.3e" % rel, flush=True)
     _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), 1024, reserved_recent=64)
     assert_same_selection(~evicted, torch.from_numpy(ref_keep), ref_imp.cpu(), 1024, 64, rtol=1e-3)
     assert (~evicted)[..., -64:].all()
@@ -119,13 +123,13 @@ def test_qwen_32k_window_pool():
     out, imp, idx, evicted = flash_evict.evict(q, k, v, 2048, reserved_recent=64, pool_kernel=5, **kw)
     # importance comes only from the last 128 queries: cheap to recompute exactly
     _, ref_imp = chunked(q, k, v, block=128, want_out=False, **kw)
-    assert rel_err(imp, ref_imp) <= 1e-3
-    # full attention output for all N rows: check first, middle and last blocks
-    rows = [(0, 256), (16384 - 128, 16384 + 128), (n - 256, n)]
-    ref_out, _ = chunked(q, k, v, block=256, query_rows=rows, value_weighted=False, **kw)
-    for r0, r1 in rows:
-        assert (out[:, :, r0:r1].float() - ref_out[:, :, r0:r1]).abs().max() <= 2e-2, (r0, r1)
+    rel = assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    print("qwen32k importance element-wise max rel err %.3e" % rel, flush=True)
+    # the full attention output is produced for all N rows: check every row of every head
     assert torch.isfinite(out).all()
+    worst = out_err_all_rows(out, q, k, v, **kw)
+    print("qwen32k out max-abs-err over all rows: %.4f" % worst, flush=True)
+    assert worst <= 2e-2
     _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), 2048, reserved_recent=64, pool_kernel=5)
     pooled = torch.nn.functional.avg_pool1d(ref_imp[..., :n - 64].reshape(-1, 1, n - 64).cpu(), 5, 1, 2)
     assert_same_selection(~evicted, torch.from_numpy(ref_keep), torch.cat(
@@ -153,6 +157,16 @@ def test_long_131k_planted_keys():
     assert keep[..., p0:p0 + 64].all(), keep[..., p0:p0 + 64].sum(-1)
     assert keep.sum(-1).eq(1024).all() and keep[..., -64:].all()
     assert torch.equal(idx, idx.sort(-1).values)
-    # spot-check: the output of the last query block against the FP32 oracle
-    ref_out, _ = chunked(q[:, :4], k[:, :1], v[:, :1], block=128, query_rows=[(n - 128, n)], value_weighted=False)
-    assert (out[:, :4, n - 128:].float() - ref_out[:, :, n - 128:]).abs().max() <= 2e-2
+    # importance against the FP32 oracle, element-wise: rows before n-1100 have recency
+    # weight exp(-0.1*(n-1-q)) <= exp(-110), exactly 0.0 in FP32, so the last 1100 rows
+    # give the whole importance
+    _, ref_imp = chunked(q, k, v, block=1100, want_out=False, recency_decay=0.1, query_rows=[(n - 1100, n)])
+    rel = assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    print("long131k importance element-wise max rel err %.3e" % rel, flush=True)
+    _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), 1024, reserved_recent=64)
+    assert_same_selection(keep, torch.from_numpy(ref_keep), ref_imp.cpu(), 1024, 64, rtol=1e-3)
+    # the output of the first, a middle and the last (planted) query blocks of every head
+    rows = [(0, 1024), (n // 2 - 512, n // 2 + 512), (n - 1024, n)]
+    ref_out, _ = chunked(q, k, v, block=1024, query_rows=rows, value_weighted=False)
+    for r0, r1 in rows:
+        assert (out[:, :, r0:r1].float() - ref_out[:, :, r0:r1]).abs().max() <= 2e-2, (r0, r1)
