@@ -43,29 +43,33 @@ def materialized(q, k, v, *, causal=True, value_weighted=True, scale=None,
 
 def chunked(q, k, v, *, causal=True, value_weighted=True, scale=None,
             recency_decay=0., observation_window=0, block=1024, heads=None, want_out=True,
-            query_rows=None):
+            query_rows=None, dtype=torch.float32):
     """Exact FP32 oracle streamed over (head, query block); never forms the N x N matrix.
 
     `heads` optionally restricts the computation to a list of (b, query head) pairs (the
     importance then only holds their contributions). `query_rows`, a list of (q0, q1)
     ranges, restricts the output rows computed (only those rows of `out` are filled; the
     importance is then only meaningful when every weighted row is included).
+    `dtype=torch.float64` evaluates the same formulas in double precision (the recency
+    weights stay the FP32 values the reference uses): a truth the FP32 rounding of the
+    logits does not blur, for inputs whose logits are so large that any FP32 evaluation,
+    the reference's included, is uncertain in the last bits.
     Returns (out or None, mass).
     """
     b, hq, n, d = q.shape
     hk = k.shape[1]
     g = hq // hk
     sc = d ** -0.5 if scale is None else scale
-    w = _weights(n, recency_decay, observation_window, q.device)
+    w = _weights(n, recency_decay, observation_window, q.device).to(dtype)
     win_lo = n - min(n, observation_window or n)
-    out = torch.zeros((b, hq, n, d), dtype=torch.float32, device=q.device) if want_out else None
-    mass = torch.zeros((b, hk, n), dtype=torch.float32, device=q.device)
+    out = torch.zeros((b, hq, n, d), dtype=dtype, device=q.device) if want_out else None
+    mass = torch.zeros((b, hk, n), dtype=dtype, device=q.device)
     pairs = heads if heads is not None else [(bi, hi) for bi in range(b) for hi in range(hq)]
     for bi, hi in pairs:
         j = hi // g
-        kf = k[bi, j].float()
-        vf = v[bi, j].float()
-        col = torch.zeros(n, dtype=torch.float32, device=q.device)
+        kf = k[bi, j].to(dtype)
+        vf = v[bi, j].to(dtype)
+        col = torch.zeros(n, dtype=dtype, device=q.device)
         if query_rows is None:
             spans = [(q0, min(n, q0 + block)) for q0 in range(0, n, block)]
         else:
@@ -74,7 +78,7 @@ def chunked(q, k, v, *, causal=True, value_weighted=True, scale=None,
             if not want_out and q1 <= win_lo:
                 continue
             kend = q1 if causal else n
-            qf = q[bi, hi, q0:q1].float()
+            qf = q[bi, hi, q0:q1].to(dtype)
             logits = torch.matmul(qf, kf[:kend].t().contiguous()) * sc
             if causal:
                 rows = torch.arange(q0, q1, device=q.device)
@@ -87,5 +91,5 @@ def chunked(q, k, v, *, causal=True, value_weighted=True, scale=None,
                 col[:kend] += (p * w[q0:q1, None]).sum(0)
         mass[bi, j] += col
     if value_weighted:
-        mass = mass * v.float().abs().sum(-1)
+        mass = mass * v.to(dtype).abs().sum(-1)
     return out, mass

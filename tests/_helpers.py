@@ -55,13 +55,16 @@ def assert_importance_close(imp, ref, rtol=1e-3, floor=1e-30):
     err = (imp - ref).abs()
     bound = rtol * ref.abs() + floor
     bad = err > bound
+    big = ref.abs() > floor
+    worst = float((err[big] / ref.abs()[big]).max()) if bool(big.any()) else 0.0
+    print("importance: max element-wise rel err %.3e over %d of %d elements above the floor %g"
+          % (worst, int(big.sum()), big.numel(), floor), flush=True)
     if bool(bad.any()):
         i = int(bad.flatten().nonzero()[0])
         raise AssertionError("importance differs beyond %g*|ref| + %g at %d of %d elements; first at flat index %d: "
                              "kernel %r, oracle %r" % (rtol, floor, int(bad.sum()), bad.numel(), i,
                                                        float(imp.flatten()[i]), float(ref.flatten()[i])))
-    big = ref.abs() > floor
-    return float((err[big] / ref.abs()[big]).max()) if bool(big.any()) else 0.0
+    return worst
 
 
 def out_err_all_rows(out, q, k, v, block=2048, **kw):

@@ -81,6 +81,38 @@ def test_materialized_matches_brute_force(c):
     torch.testing.assert_close(mass.double(), torch.tensor(bmass, dtype=torch.float64), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("c", BRUTE_CASES)
+def test_chunked_float64_matches_brute_force(c):
+    """chunked(dtype=float64) against the float64 loops, to float64 accuracy: the same
+    formulas, only the precision differs."""
+    g = torch.Generator().manual_seed(c["n"] * 37 + c["hq"])
+    q = torch.randn(c["b"], c["hq"], c["n"], c["d"], generator=g, dtype=torch.float64)
+    k = torch.randn(c["b"], c["hk"], c["n"], c["d"], generator=g, dtype=torch.float64)
+    v = torch.randn(c["b"], c["hk"], c["n"], c["d"], generator=g, dtype=torch.float64)
+    kw = dict(causal=c["causal"], value_weighted=c["vw"], recency_decay=c["decay"], observation_window=c["win"])
+    out, mass = chunked(q, k, v, block=4, dtype=torch.float64, **kw)
+    bout, bmass = brute.attention(q.tolist(), k.tolist(), v.tolist(), **kw)
+    torch.testing.assert_close(out, torch.tensor(bout, dtype=torch.float64), rtol=1e-6, atol=1e-9)
+    # the recency weights are the FP32 values of the reference (a relative 1e-7 apart from
+    # the float64 loops' weights)
+    torch.testing.assert_close(mass, torch.tensor(bmass, dtype=torch.float64), rtol=1e-6, atol=1e-9)
+
+
+def test_chunked_float64_resolves_extreme_logits():
+    """With x30 inputs the logits are ~1e3 and FP32 evaluation is off by up to ~1e-3
+    relative in the probabilities; float64 agrees with the float64 loops to 1e-9."""
+    g = torch.Generator().manual_seed(4)
+    q = (torch.randn(1, 2, 12, 16, generator=g) * 30).to(torch.float16)
+    k = (torch.randn(1, 1, 12, 16, generator=g) * 30).to(torch.float16)
+    v = torch.randn(1, 1, 12, 16, generator=g).to(torch.float16)
+    kw = dict(causal=False, value_weighted=False)
+    _, mass64 = chunked(q, k, v, block=5, dtype=torch.float64, **kw)
+    _, bmass = brute.attention(q.double().tolist(), k.double().tolist(), v.double().tolist(), **kw)
+    torch.testing.assert_close(mass64, torch.tensor(bmass, dtype=torch.float64), rtol=1e-9, atol=1e-12)
+    _, mass32 = chunked(q, k, v, block=5, **kw)
+    torch.testing.assert_close(mass32.double(), mass64, rtol=5e-3, atol=1e-6)
+
+
 # ---- textbook attention from the library (output only)
 
 @pytest.mark.parametrize("causal", [True, False])
