@@ -33,6 +33,7 @@
 //     different KV heads (the hardware deals blocks round-robin over the 8 XCDs, so each
 //     XCD's L2 sees a small set of KV heads).
 #include <math.h>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -581,7 +582,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
                         const int64_t* k_strides, const int64_t* v_strides, int dtype, float scale, int causal,
                         int value_weighted, int score, float recency_decay, int64_t window, void* workspace,
-                        size_t workspace_bytes, void* hip_stream) {
+                        size_t workspace_bytes, void* hip_stream, bool allow_timing = true) {
   if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || (score && !importance)) {
     set_error("fe_prefill: null pointer argument");
     return FE_ERR_INVALID;
@@ -688,7 +689,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
         if (x) (void)hipEventDestroy(x);
     }
   } ev;
-  const bool timed = fused_timing_enabled();
+  const bool timed = allow_timing && fused_timing_enabled();
   if (timed) {
     if (hipEventCreate(&ev.e[0]) != hipSuccess || hipEventCreate(&ev.e[1]) != hipSuccess ||
         hipEventRecord(ev.e[0], stream) != hipSuccess) {
@@ -780,4 +781,84 @@ extern "C" int fe_prefill_ws(const void* q, const void* k, const void* v, void* 
   clear_error();
   return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
                       causal, value_weighted, score, recency_decay, window, workspace, workspace_bytes, hip_stream);
+}
+
+namespace fe {
+namespace {
+
+// Replay-bias buffer of fe_prefill_static: a file-scope device array, so that entry point
+// allocates nothing. FE_STATIC_BIAS_ROWS floats (16 MiB) on every GPU the library runs on,
+// held until the process ends. Its contents persist between calls (the last call's biases);
+// the attention kernel writes every bias the replay kernel reads, so nothing is cleared.
+__device__ __align__(256) float scratch[FE_STATIC_BIAS_ROWS];
+
+// Device address of `scratch`, per device: looked up once per device, with that device
+// current, on the first fe_prefill_static call that runs on it. Host code passes this
+// address to the kernels; the array's name is only a host-side stand-in symbol.
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+constexpr int kMaxDevices = 64;
+ScratchSlot g_scratch[kMaxDevices];
+
+hipError_t static_scratch(hipStream_t stream, float** out) {
+  int cur = 0;
+  hipError_t err = hipGetDevice(&cur);
+  if (err != hipSuccess) return err;
+  int dev = cur;
+  if (stream) {
+    hipDevice_t d = 0;
+    if ((err = hipStreamGetDevice(stream, &d)) != hipSuccess) return err;
+    dev = (int)d;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&] {
+    if (dev != cur && (slot.err = hipSetDevice(dev)) != hipSuccess) return;
+    slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (slot.err == hipSuccess) slot.err = back;
+    }
+    if (slot.err == hipSuccess && !slot.ptr) slot.err = hipErrorInvalidSymbol;
+  });
+  if (slot.err != hipSuccess) return slot.err;
+  *out = (float*)slot.ptr;
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace fe
+
+extern "C" int fe_prefill_static(const void* q, const void* k, const void* v, void* out, float* importance,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                 const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                 int dtype, float scale, int causal, int value_weighted, int score,
+                                 float recency_decay, int64_t window, void* hip_stream) {
+  clear_error();
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (score && B >= 1 && Hq >= 1 && N >= 1) {
+    const int64_t R = FE_STATIC_BIAS_ROWS;
+    if (B > R || Hq > R || N > R || B * Hq > R || B * Hq * N > R) {
+      char msg[256];
+      snprintf(msg, sizeof(msg),
+               "fe_prefill_static: B*Hq*N = %.0f query rows exceed the static replay-bias buffer of %lld rows; "
+               "use fe_prefill_ws with a workspace",
+               (double)B * (double)Hq * (double)N, (long long)R);
+      set_error(msg);
+      return FE_ERR_WORKSPACE;
+    }
+    const hipError_t err = static_scratch((hipStream_t)hip_stream, &ws);
+    if (err != hipSuccess) {
+      set_error(std::string("fe_prefill_static: static buffer lookup: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+    ws_bytes = (size_t)(B * Hq * N) * sizeof(float);
+  }
+  return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
+                      causal, value_weighted, score, recency_decay, window, ws, ws_bytes, hip_stream,
+                      /*allow_timing=*/false);
 }

@@ -14,6 +14,7 @@ LIB_PATH = os.environ.get("FLASH_EVICT_LIB") or os.path.join(os.path.dirname(os.
 
 FE_DTYPE_F16 = 0
 FE_DTYPE_BF16 = 1
+FE_STATIC_BIAS_ROWS = 4194304   # include/flash_evict.h: rows of fe_prefill_static's device buffer
 
 _lock = threading.Lock()
 _lib = None
@@ -31,6 +32,9 @@ _SIGNATURES = {
     "fe_prefill_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _I64P, _I64P, _I64P,
                                      ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_float, _i64, _vp, ctypes.c_size_t, _vp]),
+    "fe_prefill_static": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _I64P, _I64P,
+                                         _I64P, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_float, _i64, _vp]),
     "fe_zero_f32": (ctypes.c_int, [_vp, _i64, _vp]),
     "fe_select_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
     "fe_select": (ctypes.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _vp, ctypes.c_int,

@@ -96,6 +96,26 @@ int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float*
                   float recency_decay, int64_t window, void* workspace, size_t workspace_bytes,
                   void* hip_stream);
 
+/*
+ * fe_prefill_ws with the replay-bias workspace taken from a fixed device buffer inside the
+ * library, so the call allocates nothing: no hipMalloc/hipFree and no allocating library
+ * routine (and no timing events: fe_fused_timing_enable does not apply to it). No
+ * counterpart in the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The buffer holds FE_STATIC_BIAS_ROWS floats (16 MiB) on every GPU the library runs on,
+ * kept until the process ends. A scoring call needs B*Hq*N <= FE_STATIC_BIAS_ROWS and
+ * otherwise fails with FE_ERR_WORKSPACE before launching anything. Every call on one GPU
+ * shares that GPU's buffer: calls that overlap on one GPU (concurrent streams or threads)
+ * race, so the caller must order them. Results: those of fe_prefill_ws (bitwise output,
+ * importance up to FP32 atomic order).
+ */
+#define FE_STATIC_BIAS_ROWS 4194304
+int fe_prefill_static(const void* q, const void* k, const void* v, void* out, float* importance,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                      const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                      int dtype, float scale, int causal, int value_weighted, int score,
+                      float recency_decay, int64_t window, void* hip_stream);
+
 /* Zero-fill n floats with a fill kernel (graph-capture safe: no hipMemset node). */
 int fe_zero_f32(float* p, int64_t n, void* hip_stream);
 

@@ -1,0 +1,101 @@
+"""fe_prefill_static, the allocation-free entry point, against fe_prefill_ws (the entry
+point it is a variant of) through the C ABI.
+
+fe_prefill_static runs the same split attention + replay kernels with the replay-bias
+buffer in a static device array of the library instead of a caller workspace. Bar: the
+attention output is bitwise equal to fe_prefill_ws's; the importance equals it up to the
+order of FP32 atomic additions (element-wise rtol 2e-6 + 1e-6 of the row maximum, the bar of
+tests/test_schedules_gpu.py). Two calls in a row, the second smaller, so a result left in
+the shared buffer by the first call cannot leak into the second. The size limit is checked
+on the host before anything is launched (CPU test).
+"""
+import ctypes
+
+import pytest
+import torch
+
+from flash_evict import _lib
+from flash_evict.prefill import _DTYPES
+
+from _helpers import seeded_randn, transposed_qkv
+
+FE_ERR_WORKSPACE = -3
+
+
+def _args(q, k, v, out, imp, causal, weighted, decay, window):
+    b, h, n, d = q.shape
+    hk = k.shape[1]
+    return (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), b, h, hk, n, d,
+            _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], d ** -0.5, int(causal),
+            int(weighted), 1, decay, min(n, window or n))
+
+
+def _run(q, k, v, causal, weighted, decay, window, static):
+    b, h, n, d = q.shape
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    imp = torch.empty((b, k.shape[1], n), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    args = _args(q, k, v, out, imp, causal, weighted, decay, window)
+    if static:
+        rc = L.fe_prefill_static(*args, stream)
+    else:
+        nbytes = L.fe_prefill_workspace_bytes(b, h, n, 1)
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        rc = L.fe_prefill_ws(*args, ws.data_ptr(), nbytes, stream)
+    _lib.check(rc, "fe_prefill_static" if static else "fe_prefill_ws")
+    torch.cuda.synchronize()
+    return out, imp
+
+
+@pytest.mark.gpu
+def test_static_entry_matches_workspace_entry_on_two_calls():
+    cases = [
+        # larger call first, then a smaller one (fewer rows, another dtype and head dim)
+        ((1, 32, 8, 4096, 128, torch.bfloat16, 20261201), dict(causal=True, weighted=True, decay=0.0, window=0)),
+        ((2, 8, 2, 1000, 64, torch.float16, 20261202), dict(causal=True, weighted=True, decay=0.05, window=0)),
+    ]
+    for (b, hq, hk, n, d, dt, seed), kw in cases:
+        print("fe_prefill_static vs fe_prefill_ws: B=%d Hq=%d Hkv=%d N=%d D=%d %s %s" % (b, hq, hk, n, d, dt, kw),
+              flush=True)
+        q, k, v = transposed_qkv(b, n, hq, hk, d, dt, seed)
+        out_s, imp_s = _run(q, k, v, static=True, **kw)
+        out_w, imp_w = _run(q, k, v, static=False, **kw)
+        assert torch.equal(out_s, out_w)
+        tol = 2e-6 * imp_w.abs() + 1e-6 * imp_w.abs().amax(-1, keepdim=True)
+        assert bool(((imp_s - imp_w).abs() <= tol).all())
+        assert torch.isfinite(out_s).all() and float(imp_s.sum()) > 0
+
+
+@pytest.mark.gpu
+def test_static_entry_without_score_and_on_the_generic_path():
+    """score=0 needs no buffer; D=96 takes the generic fused kernel (no split schedule)."""
+    q = seeded_randn((1, 4, 300, 96), torch.bfloat16, 11)
+    k = seeded_randn((1, 2, 300, 96), torch.bfloat16, 12)
+    v = seeded_randn((1, 2, 300, 96), torch.bfloat16, 13)
+    out_s, imp_s = _run(q, k, v, True, True, 0.0, 0, static=True)
+    out_w, imp_w = _run(q, k, v, True, True, 0.0, 0, static=False)
+    assert torch.equal(out_s, out_w)
+    torch.testing.assert_close(imp_s, imp_w, rtol=2e-6, atol=1e-6 * float(imp_w.abs().max()))
+    L = _lib.lib()
+    out = torch.empty_like(q)
+    args = list(_args(q, k, v, out, out, True, True, 0.0, 0))
+    args[4] = None
+    args[17] = 0                                   # score = 0: importance may be NULL
+    _lib.check(L.fe_prefill_static(*args, torch.cuda.current_stream().cuda_stream), "fe_prefill_static")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_w)
+
+
+def test_static_entry_rejects_sizes_beyond_its_buffer():
+    """B*Hq*N above FE_STATIC_BIAS_ROWS fails with FE_ERR_WORKSPACE before any HIP call
+    (the pointers below are never dereferenced)."""
+    L = _lib.lib()
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    p = ctypes.c_void_p(16)
+    R = _lib.FE_STATIC_BIAS_ROWS
+    for b, hq, n in [(1, 32, R // 32 + 1), (1, 1, R + 1), (R + 1, 1, 1), (2, 64, R // 64)]:
+        rc = L.fe_prefill_static(p, p, p, p, p, b, hq, 1, n, 64, st, st, st, 1, 0.125, 1, 1, 1, 0.0, n, None)
+        assert rc == FE_ERR_WORKSPACE, (b, hq, n, rc)
+        msg = L.fe_last_error().decode()
+        assert "static replay-bias buffer" in msg and str(R) in msg, msg
