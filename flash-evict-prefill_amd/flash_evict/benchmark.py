@@ -1,34 +1,33 @@
-"""Latency and PyTorch-allocator peak measurements of one attention layer.
+"""Latency and PyTorch-allocator peak measurements of one attention layer on MI355X.
 
-Same protocol as the reference's scripts/benchmark.py:18-126 (anishesg/flash-evict-prefill):
-per method two warm-up calls, `--repeats` calls timed with HIP events (median reported),
-then one more call with the allocator statistics reset around it; methods run in an
-order shuffled by a seeded RNG per sequence length; the report also lists the device
-kernels' registers, LDS and scratch (`kernel_resources`, standing in for the Triton
-`device_caches` dump at :104-111). Methods, for q [1,H,N,D], k/v [1,Hkv,N,D] bf16 and
-budget ceil(0.1 N):
+Protocol and report format of the reference's harnesses (scripts/benchmark.py:18-126 and
+scripts/benchmark_policies.py:26-96 in anishesg/flash-evict-prefill): each measured call gets
+two untimed warm-ups, then `--repeats` samples timed with HIP events (the median is reported),
+then one more call with the allocator's peak statistics reset around it. Within a sequence
+length the cases run in an order shuffled by a seeded RNG, the report is rewritten after
+every row, and `--require-idle` refuses to report a row while another process holds the GPU.
 
-  torch_flash            torch's fused SDPA (the reference's baseline attention)
-  hip_attention_only     prefill(score=False)      (reference: triton_attention_only)
-  fused_replay_scores    prefill()
-  fused_replay_topk      evict(budget)
-  flash_snap_w32/_w128   flash_snap(budget, window)
-  gather_kv              gather_tokens of K and V by evict's kept indices (the adapters'
-                         compaction step; not a method of the reference script)
+Modes (q [1,H,N,D], k/v [1,Hkv,N,D] bf16):
+
+  default      per length, budget ceil(0.1 N), the methods
+                 torch_flash          torch's flash SDPA (the reference's baseline attention)
+                 hip_attention_only   prefill(score=False)    (reference: triton_attention_only)
+                 fused_replay_scores  prefill()
+                 fused_replay_topk    evict(budget)
+                 flash_snap_w32/_w128 flash_snap(budget, window)
+                 gather_kv            gather_tokens of K and V by evict's kept indices (the
+                                      adapters' compaction step; not in the reference script)
+  --policies   per length torch_flash and hip_attention_only, then per budget flash_snap at
+               windows 32 and 128 and evict(budget, **policy) for every scoring policy (a
+               JSON list of {name, recency_decay, observation_window, value_weighted,
+               reserved_recent, pool_kernel} from --policy-file, else DEFAULT_POLICIES);
+               an existing report made with the same arguments is resumed
+  --kernels    the HBM-bound kernels on scaled synthetics (the headline's score array is
+               only 1 MiB, where they are launch-latency bound): achieved GB/s of
+               algorithmic bytes (each input byte read once, each output byte written once)
 
 Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
 --dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
-
-`--kernels` instead times the HBM-bound kernels on scaled synthetics (the headline's score
-array is only 1 MiB, where they are launch-latency bound) and reports achieved GB/s against
-algorithmic bytes (each input byte read once, each output byte written once).
-
-`--policies` runs the protocol of the reference's scripts/benchmark_policies.py:26-96: for
-every length, torch_flash and hip_attention_only once, then per budget flash_snap at windows
-32 and 128 and `evict(budget, **policy)` for every scoring policy (a JSON list of
-{name, recency_decay, observation_window, value_weighted, reserved_recent, pool_kernel} via
-`--policy-file`, else DEFAULT_POLICIES, the reference's published rows), in a seeded
-shuffled order, appending to an existing report with the same arguments (resumable).
 """
 import argparse
 import gc
@@ -47,47 +46,61 @@ from . import evict, gather_tokens, kernel_resources, prefill
 from . import _lib
 from .baselines import flash_attention, flash_snap
 
+SEED = 20260910
 
-@torch.inference_mode()
-def measure(fn, repeats):
-    """Median of `repeats` event-timed calls after two warm-ups, then allocator peaks of
-    one more call (scripts/benchmark.py:18-49)."""
-    for _ in range(2):
-        result = fn()
-        del result
+# Report keys of one measured row (the reference's format).
+_ALLOC_KEYS = ("allocated_before_bytes", "peak_allocated_bytes", "peak_increment_bytes", "peak_reserved_bytes",
+               "free_device_bytes_before", "total_device_bytes")
+
+
+# ---------------------------------------------------------------- measurement primitives
+
+def event_samples(fn, repeats, warmup=2):
+    """GPU milliseconds of `repeats` calls of `fn`, each bracketed by its own pair of HIP
+    events on the current stream, after `warmup` untimed calls. The events are read back
+    once, after the last sample."""
+    for _ in range(warmup):
+        fn()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(repeats):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        result = fn()
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(repeats)]
+    for begin, end in marks:
+        begin.record()
+        fn()
         end.record()
-        end.synchronize()
-        times.append(start.elapsed_time(end))
-        del result
+    torch.cuda.synchronize()
+    return [begin.elapsed_time(end) for begin, end in marks]
+
+
+def allocator_peaks(fn):
+    """Allocator statistics of one call of `fn`, made with the caching allocator emptied
+    and its peak counters reset: what the call allocates beyond its inputs."""
     gc.collect()
     torch.cuda.empty_cache()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
-    before = torch.cuda.memory_stats()
-    free_before, total = torch.cuda.mem_get_info()
-    result = fn()
+    held = torch.cuda.memory_allocated()
+    free, total = torch.cuda.mem_get_info()
+    keep = fn()
     torch.cuda.synchronize()
-    after = torch.cuda.memory_stats()
-    record = {"median_ms": statistics.median(times), "samples_ms": times,
-              "allocated_before_bytes": before["allocated_bytes.all.current"],
-              "peak_allocated_bytes": after["allocated_bytes.all.peak"],
-              "peak_increment_bytes": after["allocated_bytes.all.peak"] - before["allocated_bytes.all.current"],
-              "peak_reserved_bytes": after["reserved_bytes.all.peak"],
-              "free_device_bytes_before": free_before, "total_device_bytes": total}
-    del result
-    return record
+    stats = torch.cuda.memory_stats()
+    del keep
+    peak = stats["allocated_bytes.all.peak"]
+    values = (held, peak, peak - held, stats["reserved_bytes.all.peak"], free, total)
+    return dict(zip(_ALLOC_KEYS, values))
 
 
-def _tool_output(cmd):
-    """Text output of a diagnostic tool, or a note when it is unavailable."""
+@torch.inference_mode()
+def measure(fn, repeats):
+    """Median latency (and every sample) plus the allocator peaks of one call."""
+    samples = event_samples(fn, repeats)
+    return {"median_ms": statistics.median(samples), "samples_ms": samples, **allocator_peaks(fn)}
+
+
+# ---------------------------------------------------------------- environment records
+
+def _tool_output(cmd, timeout=20):
     try:
-        return subprocess.run(cmd, capture_output=True, text=True, timeout=20).stdout
+        return subprocess.run(cmd, capture_output=True, text=True, timeout=timeout).stdout
     except (OSError, subprocess.SubprocessError) as e:
         return "unavailable: %s" % e
 
@@ -102,27 +115,102 @@ def _git_revision():
 
 def _sources():
     here = Path(__file__).resolve().parent
-    files = [here / "prefill.py", here / "baselines.py", here / "cache.py", Path(_lib.LIB_PATH)]
+    files = [here / "prefill.py", here / "baselines.py", here / "cache.py", here / "benchmark.py", Path(_lib.LIB_PATH)]
     return {f.name: hashlib.sha256(f.read_bytes()).hexdigest() for f in files if f.exists()}
 
 
-def methods_for(q, k, v, budget):
-    """The timed callables of one sequence length."""
-    kept = {}
+def parse_gpu_pids(text):
+    """PIDs named in the JSON or table output of `amd-smi process` / `rocm-smi --showpids`."""
+    pids = set()
+    try:
+        data = json.loads(text)
+    except ValueError:
+        data = None
+    if data is not None:
+        stack = [data]
+        while stack:
+            x = stack.pop()
+            if isinstance(x, dict):
+                for key, val in x.items():
+                    tag = key.strip().upper()
+                    if tag == "PID" and isinstance(val, (int, str)) and str(val).strip().isdigit():
+                        pids.add(int(val))
+                    elif tag.startswith("PID") and tag[3:].isdigit():
+                        pids.add(int(tag[3:]))   # rocm-smi --showpids --json: {"PID1234": "name, ..."}
+                    stack.append(val)
+            elif isinstance(x, list):
+                stack.extend(x)
+        return sorted(pids)
+    for line in text.splitlines():
+        head = line.strip().split()
+        if head and head[0].isdigit() and len(head) > 1:
+            pids.add(int(head[0]))
+    return sorted(pids)
+
+
+class ContentionGuard:
+    """Records the processes holding the GPU around each row (the reference's contention
+    check, scripts/benchmark.py:60,90-115, on AMD's process queries) and, with
+    `require_idle`, refuses to report a row measured while another process was present.
+    The raw query output is kept in each row: inside a container whose PID namespace hides
+    the KFD process directory, amd-smi reports "No running processes detected" even for
+    this process, and the guard can then see no contention at all."""
+
+    QUERIES = (["amd-smi", "process", "--json"], ["rocm-smi", "--showpids", "--json"])
+
+    def __init__(self, require_idle):
+        self.require_idle = require_idle
+        self.query = None
+        for cmd in self.QUERIES:
+            out = _tool_output(cmd)
+            if not out.startswith("unavailable") and out.strip():
+                self.query = cmd
+                break
+
+    def snapshot(self):
+        """(raw tool output, PIDs other than this process)."""
+        if self.query is None:
+            return "unavailable: no amd-smi/rocm-smi process query", []
+        raw = _tool_output(self.query)
+        return raw, [p for p in parse_gpu_pids(raw) if p != os.getpid()]
+
+    def check(self, others, when):
+        if self.require_idle and others:
+            raise RuntimeError("other GPU processes %s %s the measurement; refusing an uncontended timing claim"
+                               % (others, when))
+
+
+# ---------------------------------------------------------------- cases
+
+class Case:
+    """One measured call: a sequence length, a method name, an optional budget."""
+
+    def __init__(self, n, method, budget, fn):
+        self.n, self.method, self.budget, self.fn = n, method, budget, fn
+
+    @property
+    def key(self):
+        return (self.n, self.method, self.budget)
+
+
+def layer_cases(q, k, v, n, names=None):
+    """Methods of the default mode at budget ceil(0.1 N)."""
+    budget = math.ceil(0.1 * n)
+    kept = []
 
     def gather_kv():
-        if "idx" not in kept:   # kept indices of one evict() call, made in the first warm-up
-            kept["idx"] = evict(q, k, v, budget)[2]
-        return gather_tokens(k, kept["idx"]), gather_tokens(v, kept["idx"])
-    return {
-        "torch_flash": lambda: flash_attention(q, k, v),
-        "hip_attention_only": lambda: prefill(q, k, v, score=False),
-        "fused_replay_scores": lambda: prefill(q, k, v),
-        "fused_replay_topk": lambda: evict(q, k, v, budget),
-        "flash_snap_w32": lambda: flash_snap(q, k, v, budget, 32),
-        "flash_snap_w128": lambda: flash_snap(q, k, v, budget, 128),
-        "gather_kv": gather_kv,
-    }
+        if not kept:            # the kept indices of one evict(), made in the first warm-up
+            kept.append(evict(q, k, v, budget)[2])
+        return gather_tokens(k, kept[0]), gather_tokens(v, kept[0])
+
+    table = [("torch_flash", lambda: flash_attention(q, k, v)),
+             ("hip_attention_only", lambda: prefill(q, k, v, score=False)),
+             ("fused_replay_scores", lambda: prefill(q, k, v)),
+             ("fused_replay_topk", lambda: evict(q, k, v, budget)),
+             ("flash_snap_w32", lambda: flash_snap(q, k, v, budget, 32)),
+             ("flash_snap_w128", lambda: flash_snap(q, k, v, budget, 128)),
+             ("gather_kv", gather_kv)]
+    return [Case(n, name, budget, fn) for name, fn in table if names is None or name in names]
 
 
 # Scoring policies of the reference's published policy benchmark (results/policy_benchmark.json
@@ -140,95 +228,105 @@ DEFAULT_POLICIES = [
 ]
 
 
-def policy_methods(q, k, v, budgets, policies):
-    """(name, budget, callable) of one length (scripts/benchmark_policies.py:58-67)."""
-    methods = [("torch_flash", None, lambda: flash_attention(q, k, v)),
-               ("hip_attention_only", None, lambda: prefill(q, k, v, score=False))]
+def _evict_with(q, k, v, budget, policy):
+    options = {key: val for key, val in policy.items() if key != "name"}
+    return lambda: evict(q, k, v, budget, **options)
+
+
+def policy_cases(q, k, v, n, budgets, policies):
+    """Cases of the policy mode: the two attention baselines once, then per budget the two
+    SnapKV windows and every scoring policy."""
+    cases = [Case(n, "torch_flash", None, lambda: flash_attention(q, k, v)),
+             Case(n, "hip_attention_only", None, lambda: prefill(q, k, v, score=False))]
     for budget in budgets:
-        for window in (32, 128):
-            methods.append(("snap_w%d" % window, budget, lambda b=budget, w=window: flash_snap(q, k, v, b, w)))
-        for policy in policies:
-            kw = {key: val for key, val in policy.items() if key != "name"}
-            methods.append((policy["name"], budget, lambda b=budget, kw=kw: evict(q, k, v, b, **kw)))
-    return methods
+        cases += [Case(n, "snap_w%d" % w, budget, (lambda b=budget, w=w: flash_snap(q, k, v, b, w))) for w in (32, 128)]
+        cases += [Case(n, p["name"], budget, _evict_with(q, k, v, budget, p)) for p in policies]
+    return cases
 
 
-def run_policies(args):
-    policies = DEFAULT_POLICIES
-    if args.policy_file:
-        policies = json.loads(Path(args.policy_file).read_text())
-    torch.manual_seed(20260910)
-    dest = Path(args.output)
-    dest.parent.mkdir(parents=True, exist_ok=True)
-    run_args = {"lengths": args.lengths, "budgets": args.budgets, "repeats": args.repeats, "heads": args.heads,
-                "kv_heads": args.kv_heads, "dim": args.dim}
-    report = {"args": run_args, "policies": policies, "gpu": torch.cuda.get_device_name(), "torch": torch.__version__,
-              "hip": torch.version.hip, "dtype": "bfloat16", "batch": 1, "git_revision": _git_revision(),
-              "source_sha256": _sources(),
-              "scope": "one layer; incremental allocations, inputs excluded; output, scores, selection included",
-              "rows": []}
-    if dest.exists():
-        old = json.loads(dest.read_text())
-        for key in ("args", "policies"):
-            if old.get(key) != report[key]:
-                raise ValueError("existing report %s was made with other %s" % (dest, key))
-        report = old
-    done = {(r["n"], r["method"], r["budget"]) for r in report["rows"]}
-    for n in args.lengths:
-        q = torch.randn((1, args.heads, n, args.dim), device="cuda", dtype=torch.bfloat16)
-        k = torch.randn((1, args.kv_heads, n, args.dim), device="cuda", dtype=q.dtype)
+# ---------------------------------------------------------------- runner
+
+class Report:
+    """The JSON report: header fields, rows, resumable by (n, method, budget)."""
+
+    def __init__(self, path, header, resume_keys=()):
+        self.path = Path(path)
+        self.path.parent.mkdir(parents=True, exist_ok=True)
+        self.data = dict(header, rows=[])
+        if resume_keys and self.path.exists():
+            old = json.loads(self.path.read_text())
+            for key in resume_keys:
+                if old.get(key) != header[key]:
+                    raise ValueError("existing report %s was made with other %s" % (self.path, key))
+            self.data = old
+        self.done = {(r["n"], r["method"], r["budget"]) for r in self.data["rows"]}
+
+    def add(self, row):
+        self.data["rows"].append(row)
+        self.done.add((row["n"], row["method"], row["budget"]))
+        self.data["kernel_resources"] = kernel_resources()
+        self.save()
+
+    def save(self):
+        self.path.write_text(json.dumps(self.data, indent=2) + "\n")
+
+
+def _measure_case(case, repeats, guard):
+    raw_before, others_before = guard.snapshot()
+    guard.check(others_before, "preceded")
+    row = {"n": case.n, "method": case.method, "budget": case.budget}
+    try:
+        row.update(measure(case.fn, repeats))
+    except torch.OutOfMemoryError as e:
+        row.update(error="OOM", detail=str(e))
+        gc.collect()
+        torch.cuda.empty_cache()
+    raw_after, others_after = guard.snapshot()
+    row.update(compute_processes_before=raw_before, compute_processes_after=raw_after,
+               other_compute_pids=sorted(set(others_before) | set(others_after)))
+    guard.check(others_after, "overlapped")
+    return row
+
+
+def run(report, lengths, heads, kv_heads, dim, make_cases, repeats, guard):
+    """Measure every case of every length not yet in the report, in a seeded shuffled
+    order per length (ordering effects of warm-up and temperature average out)."""
+    for n in lengths:
+        q = torch.randn((1, heads, n, dim), device="cuda", dtype=torch.bfloat16)
+        k = torch.randn((1, kv_heads, n, dim), device="cuda", dtype=torch.bfloat16)
         v = torch.randn_like(k)
-        methods = policy_methods(q, k, v, args.budgets, policies)
-        random.Random(n).shuffle(methods)
-        for name, budget, fn in methods:
-            if (n, name, budget) in done:
-                continue
-            try:
-                row = {"n": n, "method": name, "budget": budget, **measure(fn, args.repeats)}
-            except torch.OutOfMemoryError as e:
-                row = {"n": n, "method": name, "budget": budget, "error": "OOM", "detail": str(e)}
-                gc.collect()
-                torch.cuda.empty_cache()
-            report["rows"].append(row)
-            done.add((n, name, budget))
-            report["kernel_resources"] = kernel_resources()
-            dest.write_text(json.dumps(report, indent=2) + "\n")
-            print(json.dumps({key: val for key, val in row.items() if key != "samples_ms"}), flush=True)
+        todo = [c for c in make_cases(q, k, v, n) if c.key not in report.done]
+        random.Random(n).shuffle(todo)
+        for case in todo:
+            row = _measure_case(case, repeats, guard)
+            report.add(row)
+            print(json.dumps({key: val for key, val in row.items()
+                              if key not in ("samples_ms", "compute_processes_before", "compute_processes_after")}),
+                  flush=True)
         del q, k, v
         gc.collect()
         torch.cuda.empty_cache()
-    expected = len(args.lengths) * (2 + len(args.budgets) * (2 + len(policies)))
-    report["complete"] = len(done) == expected
-    dest.write_text(json.dumps(report, indent=2) + "\n")
 
 
-def _event_ms(fn, repeats):
-    """Median HIP-event time of `fn` (on torch's current stream) after two warm-ups."""
-    for _ in range(2):
-        fn()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(repeats):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        fn()
-        end.record()
-        end.synchronize()
-        times.append(start.elapsed_time(end))
-    return statistics.median(times)
+def _header(args, extra):
+    return dict(args=extra.pop("args"), gpu=torch.cuda.get_device_name(), torch=torch.__version__,
+                hip=torch.version.hip, dtype="bfloat16", batch=1, git_revision=_git_revision(),
+                source_sha256=_sources(), **extra)
 
+
+# ---------------------------------------------------------------- scaled-synthetic kernels
 
 @torch.inference_mode()
 def kernel_rows(repeats):
-    """Scaled-synthetic timings of the zero-fill, selection and gather kernels."""
+    """Scaled-synthetic timings of the zero-fill, selection, pooling and gather kernels."""
     from .prefill import _select
     rows, n, budget, recent = 256, 131072, 1024, 64
-    g = torch.Generator(device="cuda").manual_seed(20260910)
+    g = torch.Generator(device="cuda").manual_seed(SEED)
     scores = torch.rand((rows, n), device="cuda", generator=g)
     out = []
 
     def row(name, fn, nbytes, shape):
-        ms = _event_ms(fn, repeats)
+        ms = statistics.median(event_samples(fn, repeats))
         out.append({"kernel": name, "shape": shape, "median_ms": ms, "algorithmic_bytes": nbytes,
                     "GB/s": nbytes / (ms * 1e-3) / 1e9, "frac_of_8TB/s": nbytes / (ms * 1e-3) / 8e12})
         print(json.dumps(out[-1]), flush=True)
@@ -254,6 +352,8 @@ def kernel_rows(repeats):
     return out
 
 
+# ---------------------------------------------------------------- command line
+
 def main(argv=None):
     p = argparse.ArgumentParser()
     p.add_argument("--lengths", type=int, nargs="+", default=[8192, 32768, 131072])
@@ -263,52 +363,40 @@ def main(argv=None):
     p.add_argument("--repeats", type=int, default=5)
     p.add_argument("--methods", nargs="+", default=None, help="subset of the method names")
     p.add_argument("--output", default="benchmark.json")
+    p.add_argument("--require-idle", action="store_true", help="refuse rows measured while another process holds the GPU")
     p.add_argument("--kernels", action="store_true", help="time the HBM-bound kernels on scaled synthetics")
     p.add_argument("--policies", action="store_true", help="policy latency at fixed budgets")
     p.add_argument("--budgets", type=int, nargs="+", default=[256, 1024])
     p.add_argument("--policy-file", default=None, help="JSON list of scoring policies (--policies)")
     args = p.parse_args(argv)
-    if args.policies:
-        run_policies(args)
-        return
+
     if args.kernels:
-        report = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "hip": torch.version.hip,
-                  "rows": kernel_rows(args.repeats)}
-        Path(args.output).write_text(json.dumps(report, indent=2) + "\n")
+        data = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "hip": torch.version.hip,
+                "rows": kernel_rows(args.repeats)}
+        Path(args.output).write_text(json.dumps(data, indent=2) + "\n")
         return
-    torch.manual_seed(20260910)
-    output = Path(args.output)
-    output.parent.mkdir(parents=True, exist_ok=True)
-    report = {"args": vars(args), "gpu": torch.cuda.get_device_name(), "torch": torch.__version__,
-              "hip": torch.version.hip, "dtype": "bfloat16", "batch": 1, "git_revision": _git_revision(),
-              "source_sha256": _sources(), "rocm_smi_before": _tool_output(["rocm-smi"]),
-              "scope": "single attention layer; allocations include output and selection, exclude inputs",
-              "rows": []}
-    for n in args.lengths:
-        q = torch.randn((1, args.heads, n, args.dim), device="cuda", dtype=torch.bfloat16)
-        k = torch.randn((1, args.kv_heads, n, args.dim), device="cuda", dtype=q.dtype)
-        v = torch.randn_like(k)
-        budget = math.ceil(n * .1)
-        methods = methods_for(q, k, v, budget)
-        if args.methods:
-            methods = {name: fn for name, fn in methods.items() if name in args.methods}
-        # Seeded order reduces a systematic warm-up/temperature ordering effect.
-        items = list(methods.items())
-        random.Random(n).shuffle(items)
-        for name, fn in items:
-            try:
-                row = {"n": n, "method": name, "budget": budget, **measure(fn, args.repeats)}
-            except torch.OutOfMemoryError as e:
-                row = {"n": n, "method": name, "error": "OOM", "detail": str(e)}
-                gc.collect()
-                torch.cuda.empty_cache()
-            report["rows"].append(row)
-            report["kernel_resources"] = kernel_resources()
-            output.write_text(json.dumps(report, indent=2) + "\n")
-            print(json.dumps({key: val for key, val in row.items() if key != "samples_ms"}), flush=True)
-        del q, k, v
-        gc.collect()
-        torch.cuda.empty_cache()
+
+    torch.manual_seed(SEED)
+    guard = ContentionGuard(args.require_idle)
+    shape = (args.lengths, args.heads, args.kv_heads, args.dim)
+    if args.policies:
+        policies = json.loads(Path(args.policy_file).read_text()) if args.policy_file else DEFAULT_POLICIES
+        run_args = {"lengths": args.lengths, "budgets": args.budgets, "repeats": args.repeats, "heads": args.heads,
+                    "kv_heads": args.kv_heads, "dim": args.dim}
+        report = Report(args.output, _header(args, dict(
+            args=run_args, policies=policies,
+            scope="one layer; incremental allocations, inputs excluded; output, scores, selection included")),
+            resume_keys=("args", "policies"))
+        run(report, *shape, lambda q, k, v, n: policy_cases(q, k, v, n, args.budgets, policies), args.repeats, guard)
+        expected = len(args.lengths) * (2 + len(args.budgets) * (2 + len(policies)))
+        report.data["complete"] = len(report.done) == expected
+        report.save()
+        return
+
+    report = Report(args.output, _header(args, dict(
+        args=vars(args), rocm_smi_before=_tool_output(["rocm-smi"]),
+        scope="single attention layer; allocations include output and selection, exclude inputs")))
+    run(report, *shape, lambda q, k, v, n: layer_cases(q, k, v, n, args.methods), args.repeats, guard)
 
 
 if __name__ == "__main__":
