@@ -1,5 +1,5 @@
-// Token selection for gfx950: optional SnapKV average pooling, radix top-k, and the
-// keep/evict mask plus ascending kept indices, honouring the reserved recent suffix.
+// Token selection for gfx950: optional SnapKV average pooling, top-k, and the keep/evict
+// mask plus ascending kept indices, honouring the reserved recent suffix.
 //
 // Semantics follow flash_evict/prefill.py:140-180 (select_tokens / evict):
 //   past = scores[..., :n-recent]                                           (:160)
@@ -11,14 +11,25 @@
 // torch.topk leaves tie order unspecified (prefill.py:144); this build fixes it: among
 // equal scores the lower index is kept. -0.0 ties with +0.0; NaN ranks above +inf.
 //
-// Schedule: no sort at all. A three-digit (11/11/10-bit) MSB radix select per row finds
-// the threshold key T of the (budget-recent)-th largest score with LDS histograms; one
-// ordered pass then keeps key > T plus the first ties at T, and a block prefix sum gives
-// each kept token its output slot, so indices come out ascending and the mask is written
-// in the same pass. One 1024-thread workgroup per row; the passes over a row read 16-byte
-// vectors when the row is 16-byte aligned.
+// No sort anywhere. Scores map to order-preserving 32-bit keys; the (budget-recent)-th
+// largest key T is found by a three-digit (11/11/10-bit) MSB radix select, and the kept set
+// is {key > T} plus the lowest-index ties at T, so indices come out ascending from a block
+// prefix sum. One 1024-thread workgroup per row. Two schedules, both reading the row from
+// HBM once:
+//   * rows of up to kLdsRowMax past scores: the row's keys are staged in LDS by one
+//     coalesced pass, and the radix passes (restricted to a bracket taken from an evenly
+//     spaced sample of the staged keys) and the ordered output pass run from LDS;
+//   * longer rows: 512 evenly spaced 8-key segments are sampled first, and two radix
+//     selects on the sample bracket T between two keys. One pass over the row then writes
+//     the mask of every key above the bracket (kept) and below it (dropped), lists the kept
+//     indices in a small workspace, and holds the keys inside the bracket as (key, index)
+//     candidates in LDS. T is resolved exactly among the candidates, the kept candidates'
+//     mask bytes are set, and the two ascending index lists are merged into the output.
+//     A bracket that misses (possible only for unusual score layouts) falls back to the
+//     radix passes over the row in HBM: the result never depends on the sample.
 #include <math.h>
 #include <string>
+#include <type_traits>
 
 #include "fe_common.h"
 #include "fe_internal.h"
@@ -33,20 +44,51 @@ __device__ __forceinline__ u32 order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-constexpr int kSelThreads = 1024;               // threads of a selection workgroup (one row)
+constexpr int kSelThreads = 1024;                  // threads of a selection workgroup (one row)
 constexpr int kSelWaves = kSelThreads / 64;
+// Longest row staged whole in LDS. Up to 36864 keys fit (144 KiB); from 16K keys on the
+// sampled schedule is faster (8 x 32768 rows: 27.4 against 29.9 us), its single pass
+// beating the LDS schedule's bracket, three radix passes and ordered pass over every key.
+#ifndef FE_SEL_LDS_ROW_MAX
+#define FE_SEL_LDS_ROW_MAX 16384
+#endif
+constexpr int kLdsRowMax = FE_SEL_LDS_ROW_MAX;
+static_assert(kLdsRowMax <= 36864 && kLdsRowMax >= 4096, "LDS capacity; sampled rows hold at least kSamples keys");
+constexpr int kSegs = 512, kSegLen = 8;            // sample of the long-row schedule
+constexpr int kSamples = kSegs * kSegLen;
+constexpr int kCandMax = 12288;                    // (key, index) candidates held in LDS
+
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also waits for every
+// outstanding global load and store of the wave, which would stall the row's streaming
+// loads (and the mask stores) at each prefix sum; the selection kernels synchronise
+// through LDS and use a full barrier only where global memory written by one thread is
+// then read or overwritten by another.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts by 1, 2, 4 and 8
+// lanes inside each 16-lane row, then the last lane of row r added to row r+1 (row_bcast:15,
+// rows 1 and 3) and lane 31 to rows 2 and 3 (row_bcast:31). Lanes without a source add 0.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31
+  return x;
+}
 
 // Exclusive prefix sum over the threads of a selection workgroup; `total` receives the sum.
+// tmp: kSelWaves ints, 16-byte aligned.
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+  const int x = wave_inclusive_scan(v);
   if (lane == 63) tmp[w] = x;
-  __syncthreads();
+  lds_barrier();
   int before = 0;
   total = 0;
 #pragma unroll
@@ -55,151 +97,539 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total)
     before += (i < w) ? t : 0;
     total += t;
   }
-  __syncthreads();
+  lds_barrier();
   return before + x - v;
 }
 
-// out[r, i] = (sum_{j=i-k/2}^{i+k/2} past[r, j], zeros outside [0, m)) / k, summed left to
-// right (the order of torch's avg_pool kernels).
-__global__ __launch_bounds__(256) void avg_pool_kernel(const float* s, long long rs, int m, int k,
-                                                       long long blocks_per_row, float* out) {
-  const long long row = (long long)blockIdx.x / blocks_per_row;
-  const int i = (int)(((long long)blockIdx.x - row * blocks_per_row) * 256 + threadIdx.x);
-  if (i >= m) return;
-  const float* x = s + row * rs;
-  const int half = k >> 1;
-  const int lo = i - half < 0 ? 0 : i - half;
-  const int hi = i + half > m - 1 ? m - 1 : i + half;
-  float acc = 0.f;
-  for (int j = lo; j <= hi; ++j) acc += x[j];
-  out[row * (long long)m + i] = acc / (float)k;
+struct SelShared {
+  u32 prefix;
+  int kk;
+  u32 eq;
+};
+
+// Radix select over n keys (key i = get(i)) for T = the K-th largest key (1 <= K <= n),
+// need = how many keys equal to T are among the K largest, eq = how many keys equal T.
+// Only keys in [lo, hi] are histogrammed; keys above hi are counted first. Returns false
+// (T undetermined) when the K-th largest key lies outside [lo, hi]; the full range
+// [0, 0xffffffff] always succeeds.
+template <typename Get>
+__device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 hi, u32* hist, int* scan_tmp,
+                                             SelShared* sh, u32& T, int& need, int& eq) {
+  constexpr int ST = kSelThreads;
+  const int tid = threadIdx.x;
+  u32 prefix = 0, pmask = 0, eq_total = 0;
+  int kk = K;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const int nb = pass == 2 ? 1024 : 2048;
+    for (int i = tid; i < nb; i += ST) hist[i] = 0u;
+    lds_barrier();
+    int above = 0;
+#pragma unroll 8
+    for (int i = tid; i < n; i += ST) {
+      const u32 key = get(i);
+      above += key > hi ? 1 : 0;
+      if (key >= lo && key <= hi && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & (u32)(nb - 1)], 1u);
+    }
+    if (pass == 0) {
+      int n_above;
+      block_exclusive_scan(above, scan_tmp, n_above);
+      kk = K - n_above;
+    } else {
+      lds_barrier();
+    }
+    // thread t owns bins [nb - (t+1)*bpt, nb - t*bpt): thread 0 holds the highest digits
+    const int bpt = nb / ST;
+    const int hi_bin = nb - 1 - tid * bpt;
+    int local = 0;
+    for (int e = 0; e < bpt; ++e) local += (int)hist[hi_bin - e];
+    int total;
+    int cum = block_exclusive_scan(local, scan_tmp, total);
+    if (pass == 0 && (kk < 1 || kk > total)) return false;   // uniform: block totals
+    for (int e = 0; e < bpt; ++e) {
+      const int bin = hi_bin - e;
+      const int h = (int)hist[bin];
+      if (cum < kk && cum + h >= kk) {
+        sh->prefix = prefix | ((u32)bin << shift);
+        sh->kk = kk - cum;
+        sh->eq = (u32)h;
+      }
+      cum += h;
+    }
+    lds_barrier();
+    prefix = sh->prefix;
+    kk = sh->kk;
+    eq_total = sh->eq;
+    pmask |= (u32)(nb - 1) << shift;
+    lds_barrier();
+  }
+  T = prefix;
+  need = kk;
+  eq = (int)eq_total;
+  return true;
 }
 
-__global__ __launch_bounds__(kSelThreads) void select_rows_kernel(const float* src, long long src_stride, int m,
-                                                                  int K, int n, int recent, long long* idx,
-                                                                  int budget, unsigned char* mask, int invert) {
-  constexpr int ST = kSelThreads;
-  __shared__ u32 hist[2048];
-  __shared__ int scan_tmp[kSelWaves];
-  __shared__ u32 sh_prefix;
-  __shared__ int sh_kk;
-  __shared__ u32 sh_eq;
-  const int tid = threadIdx.x;
-  const long long row = blockIdx.x;
-  const float* x = src + row * src_stride;
-  const bool vec = ((uintptr_t)x & 15u) == 0;   // 16-byte loads of 4 scores
-  long long* irow = idx ? idx + row * (long long)budget : nullptr;
-  unsigned char* mrow = mask ? mask + row * (long long)n : nullptr;
-  const unsigned char keep_v = invert ? 0 : 1, drop_v = invert ? 1 : 0;
+// Bracket of a sample of kSamples keys (key i = get(i)): for sample ranks k_hi < k_lo
+// (1-based, from the top), the 22-bit prefixes of the k_hi-th and k_lo-th largest sample
+// keys, from a first radix pass shared by both ranks and a second pass per rank. key_hi is
+// the largest key with the first prefix (keys above it rank above T with high
+// probability), key_lo the smallest key with the second; without a rank the bracket is
+// open on that side.
+struct BracketShared {
+  int bin[2], rest[2], sub[2];
+};
 
-  if (K > 0) {
-    u32 prefix = 0, pmask = 0;
-    int kk = K;
-    u32 eq_total = 0;
-    for (int pass = 0; pass < 3; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const int bits = pass == 2 ? 10 : 11;
-      const int nb = 1 << bits;
-      for (int i = tid; i < nb; i += ST) hist[i] = 0u;
-      __syncthreads();
-      auto count = [&](float f) __attribute__((always_inline)) {
-        const u32 key = order_key(f);
-        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & (u32)(nb - 1)], 1u);
-      };
-      for (int i = 4 * tid; i < m; i += 4 * ST) {
-        if (vec && i + 3 < m) {
-          const float4 v = *(const float4*)(x + i);
-          count(v.x);
-          count(v.y);
-          count(v.z);
-          count(v.w);
-        } else {
-          for (int e = 0; e < 4 && i + e < m; ++e) count(x[i + e]);
-        }
+template <typename Get>
+__device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool has_hi, bool has_lo, u32* hist,
+                                               int* scan_tmp, BracketShared* sh, u32& key_hi, u32& key_lo) {
+  constexpr int ST = kSelThreads;
+  const int tid = threadIdx.x;
+  const int target[2] = {k_hi, k_lo};
+  const bool live[2] = {has_hi, has_lo};
+  const int hi_bin = 2047 - 2 * tid;            // thread t owns bins hi_bin, hi_bin - 1
+  // pass 1: top 11 bits
+  for (int i = tid; i < 2048; i += ST) hist[i] = 0u;
+  lds_barrier();
+  for (int i = tid; i < kSamples; i += ST) atomicAdd(&hist[get(i) >> 21], 1u);
+  lds_barrier();
+  int total;
+  int cum = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
+  for (int e = 0; e < 2; ++e) {
+    const int bin = hi_bin - e, h = (int)hist[bin];
+    for (int t = 0; t < 2; ++t)
+      if (live[t] && cum < target[t] && cum + h >= target[t]) {
+        sh->bin[t] = bin;
+        sh->rest[t] = target[t] - cum;
       }
-      __syncthreads();
-      // Thread t owns bins [nb - (t+1)*bpt, nb - t*bpt): thread 0 holds the highest digits.
-      const int bpt = nb / ST;
-      const int hi_bin = nb - 1 - tid * bpt;
-      int local = 0;
-      for (int e = 0; e < bpt; ++e) local += (int)hist[hi_bin - e];
-      int total;
-      int cum = block_exclusive_scan(local, scan_tmp, total);
-      for (int e = 0; e < bpt; ++e) {
-        const int bin = hi_bin - e;
-        const int h = (int)hist[bin];
-        if (cum < kk && cum + h >= kk) {
-          sh_prefix = prefix | ((u32)bin << shift);
-          sh_kk = kk - cum;
-          sh_eq = (u32)h;
-        }
-        cum += h;
-      }
-      __syncthreads();
-      prefix = sh_prefix;
-      kk = sh_kk;
-      eq_total = sh_eq;
-      pmask |= (u32)(nb - 1) << shift;
-      __syncthreads();
-    }
-    const u32 T = prefix;       // key of the K-th largest score
-    const int need_eq = kk;     // ties at T still to keep, lowest index first
-    const bool all_eq = (int)eq_total == need_eq;
-    int out_base = 0, eq_base = 0;
-    for (int c0 = 0; c0 < m; c0 += ST * 8) {
-      const int i0 = c0 + tid * 8;
-      float xv[8];
-      if (vec && i0 + 7 < m) {
-        const float4 a0 = *(const float4*)(x + i0), a1 = *(const float4*)(x + i0 + 4);
-        xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
-        xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = i0 + e < m ? x[i0 + e] : 0.f;
-      }
-      bool gt[8], eq[8];
-      int neq = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = i0 + e;
-        const bool valid = i < m;
-        const u32 key = valid ? order_key(xv[e]) : 0u;
-        gt[e] = valid && key > T;
-        eq[e] = valid && key == T;
-        neq += eq[e] ? 1 : 0;
-      }
-      int eq_before = 0;
-      if (!all_eq) {
-        int tot;
-        eq_before = block_exclusive_scan(neq, scan_tmp, tot) + eq_base;
-        eq_base += tot;
-      }
-      bool sel[8];
-      int nsel = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sel[e] = gt[e] || (eq[e] && (all_eq || eq_before < need_eq));
-        eq_before += eq[e] ? 1 : 0;
-        nsel += sel[e] ? 1 : 0;
-      }
-      int tot2;
-      int pos = block_exclusive_scan(nsel, scan_tmp, tot2) + out_base;
-      out_base += tot2;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = i0 + e;
-        if (sel[e] && irow && pos < K) irow[pos] = i;
-        pos += sel[e] ? 1 : 0;
-        if (mrow && i < m) mrow[i] = sel[e] ? keep_v : drop_v;
-      }
-    }
-  } else if (mrow) {
-    for (int i = tid; i < m; i += ST) mrow[i] = drop_v;
+    cum += h;
   }
-  for (int j = tid; j < recent; j += ST) {
+  lds_barrier();
+  // pass 2, per rank: the next 11 bits of the sample keys in that rank's bin
+  for (int t = 0; t < 2; ++t) {
+    if (!live[t]) continue;
+    const int b = sh->bin[t], r = sh->rest[t];
+    for (int i = tid; i < 2048; i += ST) hist[i] = 0u;
+    lds_barrier();
+    for (int i = tid; i < kSamples; i += ST) {
+      const u32 key = get(i);
+      if ((int)(key >> 21) == b) atomicAdd(&hist[(key >> 10) & 2047u], 1u);
+    }
+    lds_barrier();
+    int c = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
+    for (int e = 0; e < 2; ++e) {
+      const int bin = hi_bin - e, h = (int)hist[bin];
+      if (c < r && c + h >= r) sh->sub[t] = bin;
+      c += h;
+    }
+    lds_barrier();
+  }
+  key_hi = has_hi ? (((u32)sh->bin[0] << 21) | ((u32)sh->sub[0] << 10) | 0x3ffu) : 0xffffffffu;
+  key_lo = has_lo ? (((u32)sh->bin[1] << 21) | ((u32)sh->sub[1] << 10)) : 0u;
+  lds_barrier();
+}
+
+// Sample ranks bracketing the K-th largest of m keys: T is expected at rank
+// r = K * kSamples / m of the sample; take r -+ d, d = 4 sqrt(r + 1) + 8 (about four
+// standard deviations of the sample rank).
+__device__ __forceinline__ void bracket_ranks(int K, int m, int& k_hi, int& k_lo, bool& has_hi, bool& has_lo) {
+  const float r = (float)K * (float)kSamples / (float)m;
+  const float d = 4.f * sqrtf(r + 1.f) + 8.f;
+  k_hi = (int)floorf(r - d);
+  k_lo = (int)ceilf(r + d);
+  has_hi = k_hi >= 1;
+  has_lo = k_lo <= kSamples;
+}
+
+// Eight consecutive mask bytes at p (one 8-byte store when aligned and whole).
+__device__ __forceinline__ void store_mask8(unsigned char* p, const bool (&keep)[8], int valid,
+                                            unsigned char keep_v, unsigned char drop_v) {
+  if (valid == 8 && ((uintptr_t)p & 7u) == 0) {
+    unsigned long long w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w |= (unsigned long long)(keep[e] ? keep_v : drop_v) << (8 * e);
+    *(unsigned long long*)p = w;
+  } else {
+    for (int e = 0; e < valid; ++e) p[e] = keep[e] ? keep_v : drop_v;
+  }
+}
+
+// Ordered output pass: keep key > T plus the first `need_eq` keys equal to T (all of them
+// when all_eq); mask bytes of [0, m) and the ascending kept indices (positions from block
+// prefix sums over chunks of 8 keys per thread).
+template <typename Get>
+__device__ __forceinline__ void ordered_output(Get get, int m, int K, u32 T, int need_eq, bool all_eq,
+                                               long long* irow, unsigned char* mrow, unsigned char keep_v,
+                                               unsigned char drop_v, int* scan_tmp) {
+  constexpr int ST = kSelThreads;
+  const int tid = threadIdx.x;
+  int out_base = 0, eq_base = 0;
+  for (int c0 = 0; c0 < m; c0 += ST * 8) {
+    const int i0 = c0 + tid * 8;
+    bool gt[8], eq[8];
+    int neq = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool valid = i0 + e < m;
+      const u32 key = valid ? get(i0 + e) : 0u;
+      gt[e] = valid && key > T;
+      eq[e] = valid && key == T;
+      neq += eq[e] ? 1 : 0;
+    }
+    int eq_before = 0;
+    if (!all_eq) {
+      int tot;
+      eq_before = block_exclusive_scan(neq, scan_tmp, tot) + eq_base;
+      eq_base += tot;
+    }
+    bool sel[8];
+    int nsel = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sel[e] = gt[e] || (eq[e] && (all_eq || eq_before < need_eq));
+      eq_before += eq[e] ? 1 : 0;
+      nsel += sel[e] ? 1 : 0;
+    }
+    int tot2;
+    int pos = block_exclusive_scan(nsel, scan_tmp, tot2) + out_base;
+    out_base += tot2;
+    if (irow) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (sel[e] && pos < K) irow[pos] = i0 + e;
+        pos += sel[e] ? 1 : 0;
+      }
+    }
+    if (mrow && i0 < m) store_mask8(mrow + i0, sel, min(8, m - i0), keep_v, drop_v);
+  }
+}
+
+// The reserved suffix [m, m + recent) and, with nothing to select (K == 0), the dropped past.
+__device__ __forceinline__ void write_suffix(int m, int K, int recent, long long* irow, unsigned char* mrow,
+                                             unsigned char keep_v, unsigned char drop_v) {
+  const int tid = threadIdx.x;
+  if (K == 0 && mrow)
+    for (int i = tid; i < m; i += kSelThreads) mrow[i] = drop_v;
+  for (int j = tid; j < recent; j += kSelThreads) {
     if (irow) irow[K + j] = (long long)(m + j);
     if (mrow) mrow[m + j] = keep_v;
   }
+}
+
+// out[r, i] = (sum_{j=i-k/2}^{i+k/2} past[r, j], zeros outside [0, m)) / k, summed left to
+// right (the order of torch's avg_pool kernels). Each 256-thread block stages its 1024
+// outputs' inputs (plus the k/2 halo on each side) in LDS once.
+constexpr int kPoolTile = 1024;
+constexpr int kPoolHalo = 64;          // largest k/2 served from LDS (k <= 129); larger k reads HBM
+__global__ __launch_bounds__(256) void avg_pool_kernel(const float* s, long long rs, int m, int k,
+                                                       long long blocks_per_row, float* out) {
+  __shared__ float tile[kPoolTile + 2 * kPoolHalo];
+  const long long row = (long long)blockIdx.x / blocks_per_row;
+  const int i0 = (int)(((long long)blockIdx.x - row * blocks_per_row) * kPoolTile);
+  const float* x = s + row * rs;
+  const int half = k >> 1;
+  if (half <= kPoolHalo) {
+    for (int t = threadIdx.x; t < kPoolTile + 2 * half; t += 256) {
+      const int j = i0 - half + t;
+      tile[t] = (j >= 0 && j < m) ? x[j] : 0.f;
+    }
+    __syncthreads();
+  }
+  for (int t = threadIdx.x; t < kPoolTile; t += 256) {
+    const int i = i0 + t;
+    if (i >= m) break;
+    float acc = 0.f;
+    if (half <= kPoolHalo) {
+      // left to right over the window; the zero padding adds exact zeros
+      for (int j = 0; j < k; ++j) acc += tile[t + j];
+    } else {
+      const int lo = i - half < 0 ? 0 : i - half;
+      const int hi = i + half > m - 1 ? m - 1 : i + half;
+      for (int j = lo; j <= hi; ++j) acc += x[j];
+    }
+    out[row * (long long)m + i] = acc / (float)k;
+  }
+}
+
+// Rows of up to kLdsRowMax past scores: stage the keys in LDS, select, write.
+__global__ __launch_bounds__(kSelThreads) void select_lds_kernel(const float* src, long long src_stride, int m,
+                                                                 int K, int recent, long long* idx, int budget,
+                                                                 unsigned char* mask, long long mask_stride,
+                                                                 int invert) {
+  constexpr int ST = kSelThreads;
+  __shared__ u32 keys[kLdsRowMax];
+  __shared__ u32 hist[2048];
+  __shared__ __attribute__((aligned(16))) int scan_tmp[kSelWaves];
+  __shared__ SelShared sh;
+  __shared__ BracketShared bsh;
+  const int tid = threadIdx.x;
+  const long long row = blockIdx.x;
+  const float* x = src + row * src_stride;
+  long long* irow = idx ? idx + row * (long long)budget : nullptr;
+  unsigned char* mrow = mask ? mask + row * mask_stride : nullptr;
+  const unsigned char keep_v = invert ? 0 : 1, drop_v = invert ? 1 : 0;
+  if (K > 0) {
+    // 16-byte loads, four in flight per thread before any LDS store
+    if (((uintptr_t)x & 15u) == 0) {
+      const int m4 = m & ~3;
+      for (int b = 4 * tid; b < m4; b += 4 * ST * 4) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          // unconditional load (an index past the end rereads key 0 and is not stored), so
+          // that the four loads stay in flight together
+          const int i = b + u * 4 * ST;
+          v[u] = *(const float4*)(x + (i < m4 ? i : 0));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = b + u * 4 * ST;
+          if (i < m4) {
+            keys[i] = order_key(v[u].x);
+            keys[i + 1] = order_key(v[u].y);
+            keys[i + 2] = order_key(v[u].z);
+            keys[i + 3] = order_key(v[u].w);
+          }
+        }
+      }
+      for (int i = m4 + tid; i < m; i += ST) keys[i] = order_key(x[i]);
+    } else {
+      for (int i = tid; i < m; i += ST) keys[i] = order_key(x[i]);
+    }
+    lds_barrier();
+    u32 T;
+    int need, eq;
+    auto lds_key = [&](int i) { return keys[i]; };
+    // Long rows: bracket T from an evenly spaced sample of the staged keys, so the radix
+    // passes histogram only the keys inside the bracket (real scores crowd a few top-digit
+    // bins, and LDS atomics on one bin serialise); a bracket that misses T takes the
+    // passes over every key.
+    bool found = false;
+    if (m > 4 * kSamples) {
+      int k_hi, k_lo;
+      bool has_hi, has_lo;
+      bracket_ranks(K, m, k_hi, k_lo, has_hi, has_lo);
+      u32 key_hi, key_lo;
+      auto s_key = [&](int i) { return keys[(int)(((long long)i * m) >> 12)]; };   // kSamples = 4096
+      sample_bracket(s_key, k_hi, k_lo, has_hi, has_lo, hist, scan_tmp, &bsh, key_hi, key_lo);
+      found = radix_select(lds_key, m, K, key_lo, key_hi, hist, scan_tmp, &sh, T, need, eq);
+    }
+    if (!found) radix_select(lds_key, m, K, 0u, 0xffffffffu, hist, scan_tmp, &sh, T, need, eq);
+    ordered_output(lds_key, m, K, T, need, eq == need, irow, mrow, keep_v, drop_v, scan_tmp);
+  }
+  write_suffix(m, K, recent, irow, mrow, keep_v, drop_v);
+}
+
+// Rows longer than kLdsRowMax: sample bracket, one classifying pass, exact resolution among
+// the candidates. `scratch` holds K ints per row (the kept indices above the bracket); with
+// no scratch the kernel takes the radix passes over HBM directly.
+__global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float* src, long long src_stride, int m,
+                                                                    int K, int recent, long long* idx, int budget,
+                                                                    unsigned char* mask, long long mask_stride,
+                                                                    int invert, int* scratch) {
+  constexpr int ST = kSelThreads;
+  constexpr int CH = 16;                       // keys per thread per classifying step
+  __shared__ u32 skeys[kSamples];
+  __shared__ u32 hist[2048];
+  __shared__ u32 ckey[kCandMax];               // candidate keys; later the kept candidates' indices
+  __shared__ int cidx[kCandMax];
+  __shared__ __attribute__((aligned(16))) int scan_tmp[kSelWaves];
+  __shared__ SelShared sh;
+  __shared__ BracketShared bsh;
+  const int tid = threadIdx.x;
+  const long long row = blockIdx.x;
+  const float* x = src + row * src_stride;
+  long long* irow = idx ? idx + row * (long long)budget : nullptr;
+  unsigned char* mrow = mask ? mask + row * mask_stride : nullptr;
+  int* srow = scratch ? scratch + row * (long long)K : nullptr;
+  const unsigned char keep_v = invert ? 0 : 1, drop_v = invert ? 1 : 0;
+  auto hbm_key = [&](int i) { return order_key(x[i]); };
+
+  bool bracketed = K > 0 && (srow != nullptr || irow == nullptr);
+  int n_def = 0, n_cand = 0;
+  if (bracketed) {
+    // ---- sample: thread t reads keys 4(t%2) .. +3 of segment t/2. Short segments keep the
+    // sample close to uniform: a dense run of large scores (the recent tokens of an
+    // importance row) then takes no more of the sample than of the row
+    {
+      const int seg = tid >> 1, off = (tid & 1) * 4;
+      const long long start = (long long)seg * (m - kSegLen) / (kSegs - 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) skeys[4 * tid + e] = order_key(x[start + off + e]);
+    }
+    lds_barrier();
+    // ---- bracket: T is expected at sample rank r = K * kSamples / m; take ranks r -+ d,
+    // d = 4 sqrt(r + 1) + 8 (about four standard deviations of the sample rank)
+    int k_hi, k_lo;
+    bool has_hi, has_lo;
+    bracket_ranks(K, m, k_hi, k_lo, has_hi, has_lo);
+    u32 key_hi, key_lo;
+    auto s_key = [&](int i) { return skeys[i]; };
+    sample_bracket(s_key, k_hi, k_lo, has_hi, has_lo, hist, scan_tmp, &bsh, key_hi, key_lo);
+
+    // ---- classify every key once: above the bracket kept, below dropped, inside a candidate.
+    // Two chunks ahead of the one being classified are in flight (16-byte loads, 128 bytes
+    // per thread, 128 KiB per workgroup) across the classification and its prefix sum. No
+    // load sits under a branch, per-lane or uniform: the compiler waits for a load at the end
+    // of the branch around it, which would serialise the prefetch. So the aligned and
+    // unaligned rows run separate instances of the loop, and a fetch past the end of the row
+    // rereads its first keys (a valid address), which are then ignored.
+    constexpr int STEP = ST * CH;
+    auto classify_row = [&](auto aligned) __attribute__((always_inline)) {
+      constexpr bool VEC = decltype(aligned)::value;
+      float4 buf0[CH / 4], buf1[CH / 4];
+      auto fetch = [&](float4 (&b)[CH / 4], int c0) __attribute__((always_inline)) {
+        if constexpr (VEC) {
+          const int i0 = c0 + tid * CH;
+          const int ii = i0 + CH <= m ? i0 : 0;
+#pragma unroll
+          for (int u = 0; u < CH / 4; ++u) b[u] = *(const float4*)(x + ii + 4 * u);
+        }
+      };
+      auto classify = [&](float4 (&b)[CH / 4], int c0) __attribute__((always_inline)) {
+        const int i0 = c0 + tid * CH;
+        float f[CH];
+        if (VEC && i0 + CH <= m) {
+#pragma unroll
+          for (int u = 0; u < CH / 4; ++u) {
+            f[4 * u] = b[u].x;
+            f[4 * u + 1] = b[u].y;
+            f[4 * u + 2] = b[u].z;
+            f[4 * u + 3] = b[u].w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < CH; ++e) f[e] = i0 + e < m ? x[i0 + e] : 0.f;
+        }
+        fetch(b, c0 + 2 * STEP);
+        // bit e of kept / cand: key i0 + e is above / inside the bracket
+        u32 kept = 0u, cand = 0u;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          const u32 key = order_key(f[e]);
+          const bool valid = i0 + e < m;
+          kept |= (valid && key > key_hi ? 1u : 0u) << e;
+          cand |= (valid && key <= key_hi && key >= key_lo ? 1u : 0u) << e;
+        }
+        int tot;
+        const int pre = block_exclusive_scan(__builtin_popcount(kept) | (__builtin_popcount(cand) << 16), scan_tmp,
+                                             tot);   // per chunk: <= 16384 each
+        // most chunks hold no kept or candidate key in a whole wave: skip the scatter there
+        if (__any((kept | cand) != 0u)) {
+          int pd = n_def + (pre & 0xffff), pc = n_cand + (pre >> 16);
+#pragma unroll
+          for (int e = 0; e < CH; ++e) {
+            if ((kept >> e) & 1u) {
+              if (srow && pd < K) srow[pd] = i0 + e;
+              ++pd;
+            } else if ((cand >> e) & 1u) {
+              if (pc < kCandMax) {
+                ckey[pc] = order_key(f[e]);
+                cidx[pc] = i0 + e;
+              }
+              ++pc;
+            }
+          }
+        }
+        if (mrow) {
+#pragma unroll
+          for (int h = 0; h < CH / 8; ++h) {
+            const int j0 = i0 + 8 * h;
+            if (j0 + 8 <= m && ((uintptr_t)(mrow + j0) & 7u) == 0) {
+              // spread the 8 kept bits of this group into 8 bytes of 0/1
+              unsigned long long w = (unsigned long long)((kept >> (8 * h)) & 0xffu) * 0x0101010101010101ull;
+              w &= 0x8040201008040201ull;
+              w = ((w + 0x7f7f7f7f7f7f7f7full) & 0x8080808080808080ull) >> 7;
+              *(unsigned long long*)(mrow + j0) = keep_v ? w : w ^ 0x0101010101010101ull;
+            } else {
+              for (int e = 0; e < 8 && j0 + e < m; ++e)
+                mrow[j0 + e] = ((kept >> (8 * h + e)) & 1u) ? keep_v : drop_v;
+            }
+          }
+        }
+        n_def += tot & 0xffff;
+        n_cand += tot >> 16;
+      };
+      fetch(buf0, 0);
+      fetch(buf1, STEP);
+      for (int c0 = 0; c0 < m; c0 += 2 * STEP) {
+        classify(buf0, c0);
+        if (c0 + STEP < m) classify(buf1, c0 + STEP);
+      }
+    };
+    if (((uintptr_t)x & 15u) == 0)
+      classify_row(std::true_type{});
+    else
+      classify_row(std::false_type{});
+    bracketed = n_def <= K && n_def + n_cand >= K && n_cand <= kCandMax;
+  }
+
+  if (K > 0 && !bracketed) {
+    // fallback: radix passes over the row in HBM, rewriting every mask byte and index (the
+    // full barrier orders those rewrites after the classifying pass's stores)
+    __syncthreads();
+    u32 T;
+    int need, eq;
+    radix_select(hbm_key, m, K, 0u, 0xffffffffu, hist, scan_tmp, &sh, T, need, eq);
+    ordered_output(hbm_key, m, K, T, need, eq == need, irow, mrow, keep_v, drop_v, scan_tmp);
+  } else if (K > 0) {
+    __syncthreads();                           // candidates, scratch and mask of the pass are complete
+    const int K2 = K - n_def;                  // candidates still to keep
+    int n_sel = 0;
+    if (K2 > 0) {
+      u32 T;
+      int need, eq;
+      auto c_key = [&](int j) { return ckey[j]; };
+      radix_select(c_key, n_cand, K2, 0u, 0xffffffffu, hist, scan_tmp, &sh, T, need, eq);
+      const bool all_eq = eq == need;
+      int eq_base = 0;
+      for (int j0 = 0; j0 < n_cand; j0 += ST) {
+        const int j = j0 + tid;
+        const bool valid = j < n_cand;
+        const u32 key = valid ? ckey[j] : 0u;
+        const int ci = valid ? cidx[j] : 0;
+        const bool is_eq = valid && key == T;
+        int tie = 0;
+        if (!all_eq) {
+          int tot;
+          tie = block_exclusive_scan(is_eq ? 1 : 0, scan_tmp, tot) + eq_base;
+          eq_base += tot;
+        }
+        const bool sel = valid && (key > T || (is_eq && (all_eq || tie < need)));
+        int tot2;
+        const int rank = block_exclusive_scan(sel ? 1 : 0, scan_tmp, tot2) + n_sel;
+        n_sel += tot2;
+        if (sel) {
+          ckey[rank] = (u32)ci;                // ranks never pass a slot still to be read
+          if (mrow) mrow[ci] = keep_v;
+        }
+      }
+      lds_barrier();
+    }
+    if (irow) {
+      // merge the two ascending lists: kept keys above the bracket (scratch, n_def) and kept
+      // candidates (ckey as indices, n_sel); an entry's slot is its rank in its own list plus
+      // the number of entries of the other list with a lower index
+      for (int a = tid; a < n_def; a += ST) {
+        const int v = srow[a];
+        int lo = 0, hi = n_sel;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((int)ckey[mid] < v) lo = mid + 1; else hi = mid;
+        }
+        irow[a + lo] = v;
+      }
+      for (int j = tid; j < n_sel; j += ST) {
+        const int v = (int)ckey[j];
+        int lo = 0, hi = n_def;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (srow[mid] < v) lo = mid + 1; else hi = mid;
+        }
+        irow[j + lo] = v;
+      }
+    }
+  }
+  write_suffix(m, K, recent, irow, mrow, keep_v, drop_v);
 }
 
 namespace {
@@ -211,8 +641,13 @@ struct SelKernel {
 
 const SelKernel kSelKernels[] = {
     {(const void*)avg_pool_kernel, "avg_pool"},
-    {(const void*)select_rows_kernel, "select_rows"},
+    {(const void*)select_lds_kernel, "select_lds"},
+    {(const void*)select_sample_kernel, "select_sample"},
 };
+
+size_t pool_bytes(int64_t rows, int64_t n, int64_t budget, int64_t recent, int pool_kernel) {
+  return pool_kernel > 1 && budget > recent ? (size_t)rows * (size_t)(n - recent) * sizeof(float) : 0;
+}
 
 }  // namespace
 
@@ -266,9 +701,11 @@ using namespace fe;
 
 extern "C" size_t fe_select_workspace_bytes(int64_t rows, int64_t n, int64_t budget, int64_t recent,
                                             int pool_kernel) {
-  if (rows <= 0 || n <= 0 || recent < 0 || recent > n) return 0;
-  if (pool_kernel > 1 && budget > recent) return (size_t)rows * (size_t)(n - recent) * sizeof(float);
-  return 0;
+  if (rows <= 0 || n <= 0 || recent < 0 || recent > n || budget < recent || budget > n) return 0;
+  size_t bytes = pool_bytes(rows, n, budget, recent, pool_kernel);
+  // long rows: the kept indices above the sample bracket, K ints per row
+  if (n - recent > kLdsRowMax && budget > recent) bytes += (size_t)rows * (size_t)(budget - recent) * sizeof(int);
+  return bytes;
 }
 
 extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t row_stride, int64_t budget,
@@ -283,13 +720,13 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
   const int K = (int)(budget - recent);
   const float* src = scores;
   long long src_stride = rows > 1 ? row_stride : n;
-  if (pool_kernel > 1 && budget > recent) {
-    const size_t need = fe_select_workspace_bytes(rows, n, budget, recent, pool_kernel);
-    if (!workspace || workspace_bytes < need) {
+  const size_t pbytes = pool_bytes(rows, n, budget, recent, pool_kernel);
+  if (pbytes) {
+    if (!workspace || workspace_bytes < pbytes) {
       set_error("fe_select: pooling needs a workspace of fe_select_workspace_bytes() bytes");
       return FE_ERR_WORKSPACE;
     }
-    const long long bpr = (m + 255) / 256;
+    const long long bpr = (m + kPoolTile - 1) / kPoolTile;
     if (bpr * rows > 0x7fffffffLL) {
       set_error("fe_select: pooling grid too large");
       return FE_ERR_UNSUPPORTED;
@@ -304,9 +741,20 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
     src = (const float*)workspace;
     src_stride = m;
   }
-  hipLaunchKernelGGL(select_rows_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, src, src_stride, m, K,
-                     (int)n,
-                     (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out, invert ? 1 : 0);
+  if (m <= kLdsRowMax) {
+    hipLaunchKernelGGL(select_lds_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, src, src_stride, m, K,
+                       (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out, (long long)n,
+                       invert ? 1 : 0);
+  } else {
+    // scratch for the kept indices above the bracket; without room for it the kernel runs
+    // the radix passes over HBM instead
+    int* scratch = nullptr;
+    const size_t need = (size_t)rows * (size_t)K * sizeof(int);
+    if (K > 0 && workspace && workspace_bytes >= pbytes + need) scratch = (int*)((char*)workspace + pbytes);
+    hipLaunchKernelGGL(select_sample_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, src, src_stride,
+                       m, K, (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out,
+                       (long long)n, invert ? 1 : 0, scratch);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error(std::string("fe_select: select launch: ") + hipGetErrorString(err));

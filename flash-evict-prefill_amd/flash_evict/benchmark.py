@@ -340,6 +340,11 @@ def kernel_rows(repeats):
     sel_bytes = rows * n * 4 + rows * n + rows * budget * 8
     row("select (top-k + mask + indices)", lambda: _select(scores, budget, recent, 1, False), sel_bytes,
         "%d rows x %d, budget %d, recent %d" % (rows, n, budget, recent))
+    for r2, n2 in ((8, 32768), (256, 32768)):       # the headline's rows; rows staged whole in LDS
+        s2 = torch.rand((r2, n2), device="cuda", generator=g)
+        b2 = r2 * n2 * 4 + r2 * n2 + r2 * budget * 8
+        row("select %d x %d" % (r2, n2), lambda s2=s2: _select(s2, budget, recent, 1, True), b2,
+            "%d rows x %d, budget %d, recent %d (evict mask)" % (r2, n2, budget, recent))
     pool_bytes = sel_bytes + 2 * rows * (n - recent) * 4
     row("select with pool 5", lambda: _select(scores, budget, recent, 5, False), pool_bytes,
         "%d rows x %d, budget %d, recent %d, pool 5 (pooled scores written and read once)" % (rows, n, budget, recent))

@@ -34,8 +34,8 @@ def test_kernel_mode(tmp_path):
     out = tmp_path / "k.json"
     benchmark.main(["--kernels", "--repeats", "2", "--output", str(out)])
     rows = json.loads(out.read_text())["rows"]
-    assert [r["kernel"] for r in rows] == ["zero_f32", "select (top-k + mask + indices)", "select with pool 5",
-                                          "gather_tokens"]
+    assert [r["kernel"] for r in rows] == ["zero_f32", "select (top-k + mask + indices)", "select 8 x 32768",
+                                          "select 256 x 32768", "select with pool 5", "gather_tokens"]
     assert all(r["median_ms"] > 0 and r["GB/s"] > 0 for r in rows)
 
 

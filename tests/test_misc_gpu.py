@@ -113,7 +113,13 @@ def test_output_independent_of_scoring_and_deterministic(d, window):
 def test_kernel_resources():
     res = flash_evict.kernel_resources()
     names = {r["kernel"] for r in res}
-    assert "fused_fast<bf16,128>" in names and "select_rows" in names
+    assert "fused_fast<bf16,128>" in names and {"select_lds", "select_sample", "avg_pool"} <= names
+    # the selection kernels hold a whole row's keys (LDS schedule) or the sample and the
+    # candidate pairs (sampled schedule) in static LDS, within the 160 KiB of a CU
+    sel = {r["kernel"]: r for r in res if r["kernel"].startswith("select_")}
+    assert 16384 * 4 <= sel["select_lds"]["lds_static_bytes"] <= 160 * 1024
+    assert 4096 * 4 + 2 * 12288 * 4 <= sel["select_sample"]["lds_static_bytes"] <= 160 * 1024
+    assert all(r["scratch_bytes_per_thread"] == 0 for r in sel.values())
     fast = [r for r in res if r["kernel"] == "fused_fast<bf16,128>"][0]
     # K/V double buffers of two 64-key tiles (8 x 64 rows x 256 B) plus the column-sum
     # exchange of the twelve waves, all static LDS; three waves per SIMD

@@ -69,3 +69,66 @@ def test_noncontiguous_and_special_values():
     idx, keep = select_tokens(lead, 8, recent=2)
     assert idx.shape == (2, 3, 4, 8) and keep.shape == (2, 3, 4, 64)
     assert torch.equal(idx.cpu(), select_tokens(lead.cpu(), 8, recent=2)[0])
+
+
+def _host_equal(x, budget, recent=0, pool=1):
+    idx_d, keep_d = select_tokens(x.cuda(), budget, recent=recent, pool_kernel=pool)
+    idx_h, keep_h = select_tokens(x, budget, recent=recent, pool_kernel=pool)
+    assert torch.equal(idx_d.cpu(), idx_h) and torch.equal(keep_d.cpu(), keep_h)
+
+
+@pytest.mark.parametrize("n,budget,recent", [(16384, 1024, 0), (16385, 1024, 0), (16384 + 64, 1024, 64),
+                                             (16385 + 64, 1024, 64), (9000, 900, 0)])
+def test_schedule_boundary(n, budget, recent):
+    """The last row length staged whole in LDS and the first sampled one (past = n - recent)."""
+    print(f"select boundary n={n} budget={budget} recent={recent}", flush=True)
+    x = torch.rand((3, n), generator=torch.Generator().manual_seed(n)) * 10
+    _host_equal(x, budget, recent)
+
+
+@pytest.mark.parametrize("n,decay", [(131072, 0.1), (65536, 0.01), (200003, 1.0)])
+def test_sampled_schedule_on_importance_like_rows(n, decay):
+    """Rows shaped like decayed importance: a dense run of large scores at the end of the row,
+    a noise floor elsewhere, an attention sink at token 0."""
+    print(f"select importance-like n={n} decay={decay}", flush=True)
+    g = torch.Generator().manual_seed(n)
+    t = torch.arange(n - 1, -1, -1, dtype=torch.float64)
+    x = ((-decay * t).exp() + torch.rand((4, n), generator=g, dtype=torch.float64) * 1e-3).float()
+    x[:, 0] = 5.0
+    for budget, recent in ((1024, 64), (1024, 0), (17, 5), (n // 10, 64)):
+        _host_equal(x, budget, recent)
+
+
+def test_sampled_schedule_fallbacks():
+    """Brackets that cannot hold the threshold (a large budget, heavy ties) and a call with no
+    room for the schedule's scratch take the radix passes over HBM: the same result."""
+    print("select fallbacks", flush=True)
+    g = torch.Generator().manual_seed(3)
+    x = torch.rand((2, 50000), generator=g)
+    _host_equal(x, 40000, 100)                                    # large K
+    _host_equal(torch.randint(0, 3, (2, 80000), generator=g).float(), 5000, 0)   # ties
+    import ctypes
+    from flash_evict import _lib
+    L = _lib.lib()
+    xd = x.cuda()
+    idx = torch.empty((2, 1024), dtype=torch.int64, device="cuda")
+    keep = torch.empty((2, 50000), dtype=torch.bool, device="cuda")
+    need = L.fe_select_workspace_bytes(2, 50000, 1024, 0, 1)     # rows past 16384 keys: scratch
+    assert need == 2 * 1024 * 4
+    _lib.check(L.fe_select(xd.data_ptr(), 2, 50000, 50000, 1024, 0, 1, idx.data_ptr(), keep.data_ptr(), 0,
+                           None, 0, torch.cuda.current_stream().cuda_stream), "fe_select")
+    hidx, hkeep = select_tokens(x, 1024)
+    assert torch.equal(idx.cpu(), hidx) and torch.equal(keep.cpu(), hkeep)
+
+
+def test_sampled_schedule_special_values():
+    print("select special values, long rows", flush=True)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn((3, 70001), generator=g)
+    x[0, ::997] = float("nan")
+    x[1, ::1013] = float("inf")
+    x[1, 5::1013] = -float("inf")
+    x[2, ::2] = -0.0
+    x[2, 1::2] = 0.0
+    for budget, recent in ((1024, 64), (3000, 0)):
+        _host_equal(x, budget, recent)
