@@ -58,16 +58,11 @@ constexpr int kSegs = 512, kSegLen = 8;            // sample of the long-row sch
 constexpr int kSamples = kSegs * kSegLen;
 constexpr int kCandMax = 12288;                    // (key, index) candidates held in LDS
 
-// Workgroup barrier that orders LDS accesses only. __syncthreads() also waits for every
-// outstanding global load and store of the wave, which would stall the row's streaming
-// loads (and the mask stores) at each prefix sum; the selection kernels synchronise
-// through LDS and use a full barrier only where global memory written by one thread is
-// then read or overwritten by another.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// The selection kernels synchronise through LDS with lds_barrier() (fe_common.h):
+// __syncthreads() also waits for every outstanding global load and store of the wave, which
+// would stall the row's streaming loads (and the mask stores) at each prefix sum. A full
+// barrier is used only where global memory written by one thread is then read or
+// overwritten by another.
 
 // Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts by 1, 2, 4 and 8
 // lanes inside each 16-lane row, then the last lane of row r added to row r+1 (row_bcast:15,
