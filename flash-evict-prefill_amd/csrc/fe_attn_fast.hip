@@ -21,8 +21,9 @@
 //     from the V tile (rows of one 32-channel tile) with two ds_read_b64_tr_b16 transposing
 //     reads; the key order of the read matches the S^T accumulator row order that becomes
 //     P^T.
-//   * Row maxima use v_maximum3_f32 (no NaN canonicalisation); O is rescaled only when
-//     some row's running max actually rises (wave vote).
+//   * A row's reference max is the exact max of its first tile and changes only when a
+//     later tile's probabilities could overflow; the output is normalised by the sum of the
+//     probabilities as rounded for P@V (see t1_step), so O is rarely rescaled.
 //   * Masked logits are set to -inf in place, so masking costs one compare/select per
 //     element on diagonal and ragged tiles only.
 #include <math.h>
@@ -203,8 +204,15 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
   };
 
   f32x16 o[NDT];
-  float m_run = NEG_INF, l_run = 0.f;
+  float m_run = NEG_INF;                         // reference max of the row (log2 units)
+  float l_run = 0.f;                             // FP32 sum of the probabilities (replay rows)
+  float l_rnd = 0.f;                             // sum of the probabilities as rounded for P@V
   float nm = 0.f;                                // -m_run, or 0 while m_run is -inf
+  bool fresh = true;                             // no tile of this row tile seen yet
+  // Only rows the replay visits need the FP32 sum (their replay bias); it is wave-uniform.
+  const bool exact_l = a.score && tv && q0 + 31 >= a.win_lo;
+  u32 ones2;                                     // (1, 1) of the element type, for E::sum2
+  asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
 
@@ -224,13 +232,34 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
     }
   };
   // One 64-key tile: S^T = K Q^T (two 32-key accumulators; lanes hold queries), mask on
-  // diagonal and ragged tiles, exact running max with O/l rescale only when some row's max
-  // rose, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
-  auto t1_step = [&](int it, int BUF, int SLOT) __attribute__((always_inline)) {
-    const int kb = it * BN;
-    if (kb > wave_hi) return;
-
-    f32x16 sacc[2];
+  // diagonal and ragged tiles, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
+  //
+  // Reference max. The row's first tile sets m to its exact max, so that tile's largest
+  // probability is exactly 1 and every row sum is at least 1. Later tiles keep m; their
+  // probabilities may exceed 1 where the row's max has risen. The output is O divided by
+  // l_rnd, the sum of the probabilities exactly as rounded for the P@V product, so a row
+  // dominated by one key returns that key's value whatever m is (dividing by the unrounded
+  // sum would leave that key's rounding error, up to 2^-9 relative in bf16, in the output).
+  // The replay bias needs the FP32 sum of the unrounded probabilities (l_run, replay rows
+  // only): b = m + log2 l_run does not depend on the choice of m. A tile some lane of which
+  // sums to more than E::kMaxTileSum (inf included) takes a new exact max, rescales O and
+  // both sums and recomputes its probabilities, which are then at most 1. For random inputs
+  // that happens on a few percent of tiles, where following the exact running max rescaled
+  // O on ~40% of them, and no tile spends instructions on a row max.
+  auto exact_max = [&](const f32x16(&sacc)[2]) __attribute__((always_inline)) -> float {
+    // max over the 32 keys of this lane and the other half-wave: two chains of three-input
+    // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
+    float mc[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      mc[s] = vmax(vmax(sacc[s][0], sacc[s][1]), sacc[s][2]);
+#pragma unroll
+      for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
+    }
+    return half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15]))) * a.scale_log2;
+  };
+  // S^T of one tile into sacc, masked on diagonal and ragged tiles
+  auto qk_tile = [&](int kb, int BUF, int SLOT, f32x16(&sacc)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -246,7 +275,6 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
         FE_PRIO_LO();
       }
     }
-
     if (kb + BN - 1 > lo_lim) {
       // key kb + 32s + 8(i/4) + 4h + i%4 is visible iff its offset within the tile is at most
       // rel: one subtraction per lane, then compares against inline constants
@@ -257,31 +285,14 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
         for (int i = 0; i < 16; ++i)
           sacc[s][i] = 32 * s + 8 * (i >> 2) + (i & 3) <= rel ? sacc[s][i] : NEG_INF;
     }
-    // max over the 32 keys of this lane and the other half-wave: two chains of three-input
-    // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
-    float mc[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      mc[s] = vmax(vmax(sacc[s][0], sacc[s][1]), sacc[s][2]);
-#pragma unroll
-      for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
-    }
-    const float mr = half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15])));
-    // Exact running max: the dominant probability of a row stays exactly 1 before it is
-    // rounded to the input dtype (a stale max would cost up to 2^-9 relative error on the
-    // term that dominates a peaked row). O and l are only touched when some row's max rose.
-    const float mt = mr * a.scale_log2;
-    if (__any(mt > m_run)) {
-      const float mn = vmax(m_run, mt);
-      const float corr = mn > m_run ? fast_exp2(m_run - mn) : 1.f;
-      l_run *= corr;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      m_run = mn;
-      nm = mn == NEG_INF ? 0.f : -mn;
-    }
-
-    u32x4 pb[4];
+  };
+  // P = exp2(S*scale - m) packed to the input dtype, with per-lane partial sums of the
+  // rounded probabilities (pr). The EXACT flavour (replay rows) also returns the lane's FP32
+  // sum of the unrounded ones. The two flavours are separate code under a wave-uniform
+  // branch: folded into one, the compiler turns the condition into a select per element.
+  // S is consumed in place.
+  auto probs = [&](auto exact_tag, f32x16(&sacc)[2], u32x4(&pb)[4], float(&pr)[4]) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
     float ps[4];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -289,17 +300,60 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         p[i] = fast_exp2(fmaf(sacc[s][i], a.scale_log2, nm));
-        if (s == 0 && i < 4)
-          ps[i] = p[i];
-        else
-          ps[i & 3] += p[i];
+        if constexpr (EXACT) ps[i & 3] = s == 0 && i < 4 ? p[i] : ps[i & 3] + p[i];
       }
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2)
         pb[2 * s + c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
                                  E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
     }
-    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = E::sum2(pb[0][j], ones2, 0.f);
+#pragma unroll
+      for (int c = 1; c < 4; ++c) pr[j] = E::sum2(pb[c][j], ones2, pr[j]);
+    }
+    if constexpr (EXACT)
+      return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    else
+      return 0.f;
+  };
+  auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
+    const int kb = it * BN;
+    if (kb > wave_hi) return;
+
+    f32x16 sacc[2];
+    qk_tile(kb, BUF, SLOT, sacc);
+    if (fresh) {
+      // first tile of the row tile (O and the sums are still zero): exact max, no rescale
+      const float mt = exact_max(sacc);
+      m_run = mt;
+      nm = mt == NEG_INF ? 0.f : -mt;
+      fresh = false;
+    }
+    u32x4 pb[4];
+    float pr[4];
+    float le = probs(exact_tag, sacc, pb, pr);
+    // overflow guard on a lane's tile sum: the FP32 sum where it exists (ready right after the
+    // exponentials), else the rounded one
+    const float guard = decltype(exact_tag)::value ? le : (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if (__any(guard > E::kMaxTileSum)) {
+      // S again (the tile is still in LDS), the new exact max, O and both sums rescaled,
+      // probabilities recomputed: now all at most 1
+      qk_tile(kb, BUF, SLOT, sacc);
+      const float mt = exact_max(sacc);
+      const float mn = vmax(m_run, mt);
+      const float corr = mn > m_run ? fast_exp2(m_run - mn) : 1.f;
+      l_run *= corr;
+      l_rnd *= corr;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+      m_run = mn;
+      nm = mn == NEG_INF ? 0.f : -mn;
+      le = probs(exact_tag, sacc, pb, pr);
+    }
+    l_rnd += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (decltype(exact_tag)::value) l_run += le;
 
     if constexpr (NW > 8) {
       // three waves per SIMD cover the V read latency; no prefetch (16 fewer registers)
@@ -340,23 +394,31 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
         dma_v(sl * BN, lds_v0 + sl * TILE);
       }
   }
-  for (int it = 0; it < ntiles; it += 4) {
-    t1_sync(it, 0);
-    t1_step(it, 0, 0);
-    if (it + 1 < ntiles) t1_step(it + 1, 0, 1);
-    if (it + 2 < ntiles) {
-      t1_sync(it + 2, 1);
-      t1_step(it + 2, 1, 0);
-      if (it + 3 < ntiles) t1_step(it + 3, 1, 1);
+  // The tile loop is instantiated twice, with and without the FP32 sum of the replay rows,
+  // and each wave runs one of them: the choice is made once per wave, not per tile.
+  auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
+    for (int it = 0; it < ntiles; it += 4) {
+      t1_sync(it, 0);
+      t1_step(exact_tag, it, 0, 0);
+      if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
+      if (it + 2 < ntiles) {
+        t1_sync(it + 2, 1);
+        t1_step(exact_tag, it + 2, 1, 0);
+        if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+      }
     }
-  }
+  };
+  if (exact_l)
+    t1_loop(std::true_type{});
+  else
+    t1_loop(std::false_type{});
 
   // ---------------- finish rows
-  const float l_tot = half_swap_sum(l_run);
+  const float l_tot = half_swap_sum(l_run);      // replay rows only
   {
     const int qi = q0 + l32;
     if (tv && qi < N) {
-      const float inv = 1.f / l_tot;
+      const float inv = 1.f / half_swap_sum(l_rnd);
       u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * DP;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {

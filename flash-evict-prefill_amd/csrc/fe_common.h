@@ -19,6 +19,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // Element tags: storage is always 16-bit; the tag selects MFMA flavour and rounding.
 struct BF16 {
   typedef __bf16 scalar;
+  // Largest per-lane sum of one tile's probabilities (relative to a row's reference max)
+  // the attention kernels accept before taking a new reference max: bf16 and the FP32
+  // accumulation have FP32's range, and 2^32 leaves room for long rows of large values.
+  static constexpr float kMaxTileSum = 4294967296.f;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -31,10 +35,19 @@ struct BF16 {
   static __device__ __forceinline__ float to_f32(unsigned short bits) {
     return __uint_as_float(((u32)bits) << 16);
   }
+  // acc + lo + hi of a packed pair, the rounded values (v_dot2c_f32_bf16 against ones2 =
+  // (1, 1) of the type, kOnes2, which callers keep in a scalar register: as a 32-bit
+  // literal operand v_dot2c issues measurably slower)
+  static constexpr u32 kOnes2 = 0x3f803f80u;
+  static __device__ __forceinline__ float sum2(u32 packed, u32 ones2, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), __builtin_bit_cast(bf16x2, ones2), acc,
+                                           false);
+  }
 };
 
 struct F16 {
   typedef _Float16 scalar;
+  static constexpr float kMaxTileSum = 32768.f;  // probabilities stay below the fp16 maximum
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -45,6 +58,10 @@ struct F16 {
   }
   static __device__ __forceinline__ float to_f32(unsigned short bits) {
     return (float)__builtin_bit_cast(_Float16, bits);
+  }
+  static constexpr u32 kOnes2 = 0x3c003c00u;
+  static __device__ __forceinline__ float sum2(u32 packed, u32 ones2, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, ones2), acc, false);
   }
 };
 

@@ -1,0 +1,85 @@
+"""GPU tests of the attention kernel's reference max and its output normalisation.
+
+The kernel keeps a row's reference max m at the exact max of the row's first key tile and
+moves it only when a tile's probabilities relative to m could overflow (a lane's tile sum
+above 2^32 for bf16, 2^15 for fp16). It divides the output by the sum of the probabilities
+exactly as rounded for the P@V product. The reference's kernel (flash_evict/prefill.py:37-60)
+follows the running max exactly instead, so the key that dominates a row enters P@V as 1.0.
+These tests plant such a key after the first tile:
+
+  * a jump of ~2^20 (below the guard): the dominant key's probability is far from 1 and is
+    rounded to bf16. With the rounded-sum normalisation the output of every dominated row
+    equals that key's value row bit for bit; dividing by the unrounded sum instead would
+    leave the probability's rounding error (up to 2^-9 relative) in the output, which
+    changes some of these bf16 outputs by an ulp;
+  * a jump of ~2^56 (above the guard): the tile takes a new exact max and is recomputed;
+    the same bitwise property holds;
+  * fp16, whose guard is 2^15, across both regimes: output and importance against the
+    float64 oracle.
+
+Importance is checked element-wise against the oracle in every case.
+"""
+import math
+
+import pytest
+import torch
+
+from flash_evict import prefill
+from oracle.attention import chunked
+from _helpers import assert_importance_close
+from test_schedules_gpu import _run
+
+pytestmark = pytest.mark.gpu
+
+LOG2E = 1.4426950408889634
+
+
+def _planted(n, hq, hk, d, dtype, kp, jump_log2, seed):
+    """Queries along one direction u (a slightly different length per row); keys with small
+    logits except key kp, whose logit is ~jump_log2 (log2 units) above them for every query;
+    values of the planted key in [1, 8) in magnitude, so a dominated row's bf16/fp16 output
+    is that row of V exactly."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm() * math.sqrt(d)                              # |u|^2 = d
+    rows = 1.0 + 0.05 * torch.arange(n, dtype=torch.float32) / n  # per-row length: varied rounding
+    q = (u[None, None, :] * rows[None, :, None]).expand(hq, n, d).clone()
+    k = 0.5 * torch.randn((hk, n, d), generator=g)
+    beta = jump_log2 / (math.sqrt(d) * LOG2E)                   # logit(kp) = beta * sqrt(d) per unit row
+    k[:, kp] = beta * u
+    v = torch.randn((hk, n, d), generator=g)
+    mag = 1.0 + 6.0 * torch.rand((hk, d), generator=g)
+    sign = torch.where(torch.rand((hk, d), generator=g) < 0.5, -1.0, 1.0)
+    v[:, kp] = sign * mag
+    return (q[None].to(dtype).cuda(), k[None].to(dtype).cuda(), v[None].to(dtype).cuda())
+
+
+@pytest.mark.parametrize("jump_log2", [24.0, 60.0])
+@pytest.mark.parametrize("use_ws", [True, False])
+def test_dominant_key_after_first_tile_bf16(jump_log2, use_ws):
+    n, hq, hk, d, kp = 1024, 2, 1, 128, 300
+    print("planted dominant key bf16: n=%d kp=%d jump 2^%g use_ws=%s" % (n, kp, jump_log2, use_ws), flush=True)
+    q, k, v = _planted(n, hq, hk, d, torch.bfloat16, kp, jump_log2, seed=11)
+    out, imp = _run(q, k, v, True, True, 0.0, 0, use_ws=use_ws)
+    assert torch.isfinite(out).all() and torch.isfinite(imp).all()
+    # every row that sees key kp returns its value row exactly
+    dom = out[0, :, kp:, :]
+    want = v[0, 0, kp][None, None, :].expand_as(dom)
+    bad = (dom != want).sum().item()
+    assert bad == 0, "%d of %d outputs of dominated rows differ from the dominant value" % (bad, dom.numel())
+    ref_out, ref_imp = chunked(q, k, v, block=512, dtype=torch.float64)
+    assert (out.float() - ref_out).abs().max().item() <= 2e-2
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+
+
+@pytest.mark.parametrize("jump_log2", [10.0, 30.0])
+def test_dominant_key_after_first_tile_fp16(jump_log2):
+    n, hq, hk, d, kp = 1024, 4, 2, 64, 700
+    print("planted dominant key fp16: n=%d kp=%d jump 2^%g" % (n, kp, jump_log2), flush=True)
+    q, k, v = _planted(n, hq, hk, d, torch.float16, kp, jump_log2, seed=12)
+    out, imp = prefill(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(imp).all()
+    ref_out, ref_imp = chunked(q, k, v, block=512, dtype=torch.float64)
+    assert (out.float() - ref_out).abs().max().item() <= 5e-3
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
