@@ -19,14 +19,15 @@
 //   * rows of up to kLdsRowMax past scores: the row's keys are staged in LDS by one
 //     coalesced pass, and the radix passes (restricted to a bracket taken from an evenly
 //     spaced sample of the staged keys) and the ordered output pass run from LDS;
-//   * longer rows: 512 evenly spaced 8-key segments are sampled first, and two radix
-//     selects on the sample bracket T between two keys. One pass over the row then writes
-//     the mask of every key above the bracket (kept) and below it (dropped), lists the kept
-//     indices in a small workspace, and holds the keys inside the bracket as (key, index)
-//     candidates in LDS. T is resolved exactly among the candidates, the kept candidates'
-//     mask bytes are set, and the two ascending index lists are merged into the output.
-//     A bracket that misses (possible only for unusual score layouts) falls back to the
-//     radix passes over the row in HBM: the result never depends on the sample.
+//   * longer rows (up to kBitRowMax): 512 evenly spaced 8-key segments are sampled first,
+//     and two radix selects on the sample bracket T between two keys. One pass over the
+//     row, with no workgroup barrier, then writes the mask of every key above the bracket
+//     (kept) and below it (dropped), records the kept keys in an LDS bitmap, and holds the
+//     keys inside the bracket as (key, index) candidates in LDS. T is resolved exactly among
+//     the candidates (ties by index), their bits and mask bytes are set, and one ordered
+//     pass over the bitmap writes the ascending indices. A bracket that misses (possible
+//     only for unusual score layouts), and longer rows, take the radix passes over the row
+//     in HBM: the result never depends on the sample.
 #include <math.h>
 #include <string>
 #include <type_traits>
@@ -44,6 +45,15 @@ __device__ __forceinline__ u32 order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The float whose order key is k, for keys from -inf (0x007fffff) to +inf (0xff800000);
+// keys above +inf give a NaN pattern, with which every ordered compare is false. For
+// thresholds between keys: v >= key_float(k) holds exactly when order_key(v) >= k, for every
+// non-NaN v (-0 == +0 under IEEE compares, and key 0x7fffffff, which no float has, maps to
+// -0 so that both zeros pass). FP32 denormals take part in compares as numbers.
+__device__ __forceinline__ float key_float(u32 k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 constexpr int kSelThreads = 1024;                  // threads of a selection workgroup (one row)
 constexpr int kSelWaves = kSelThreads / 64;
 // Longest row staged whole in LDS. Up to 36864 keys fit (144 KiB); from 16K keys on the
@@ -57,6 +67,7 @@ static_assert(kLdsRowMax <= 36864 && kLdsRowMax >= 4096, "LDS capacity; sampled 
 constexpr int kSegs = 512, kSegLen = 8;            // sample of the long-row schedule
 constexpr int kSamples = kSegs * kSegLen;
 constexpr int kCandMax = 12288;                    // (key, index) candidates held in LDS
+constexpr int kBitRowMax = 262144;                 // longest row of the sampled schedule (32 KiB bitmap)
 
 // The selection kernels synchronise through LDS with lds_barrier() (fe_common.h):
 // __syncthreads() also waits for every outstanding global load and store of the wave, which
@@ -106,15 +117,26 @@ struct SelShared {
 // need = how many keys equal to T are among the K largest, eq = how many keys equal T.
 // Only keys in [lo, hi] are histogrammed; keys above hi are counted first. Returns false
 // (T undetermined) when the K-th largest key lies outside [lo, hi]; the full range
-// [0, 0xffffffff] always succeeds.
+// [0, 0xffffffff] always succeeds. With `within` (every key lies in [lo, hi]) the leading
+// digits that lo and hi share are known and their passes are skipped.
 template <typename Get>
 __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 hi, u32* hist, int* scan_tmp,
-                                             SelShared* sh, u32& T, int& need, int& eq) {
+                                             SelShared* sh, u32& T, int& need, int& eq, bool within = false) {
   constexpr int ST = kSelThreads;
   const int tid = threadIdx.x;
   u32 prefix = 0, pmask = 0, eq_total = 0;
   int kk = K;
-  for (int pass = 0; pass < 3; ++pass) {
+  int first = 0;
+  if (within && (lo >> 21) == (hi >> 21)) {
+    first = 1;
+    pmask = 0xffe00000u;
+    if ((lo >> 10) == (hi >> 10)) {
+      first = 2;
+      pmask = 0xfffffc00u;
+    }
+    prefix = lo & pmask;
+  }
+  for (int pass = first; pass < 3; ++pass) {
     const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
     const int nb = pass == 2 ? 1024 : 2048;
     for (int i = tid; i < nb; i += ST) hist[i] = 0u;
@@ -233,6 +255,28 @@ __device__ __forceinline__ void bracket_ranks(int K, int m, int& k_hi, int& k_lo
   k_lo = (int)ceilf(r + d);
   has_hi = k_hi >= 1;
   has_lo = k_lo <= kSamples;
+}
+
+// f[e] for a per-lane index e without indexing the register array (which would place it in
+// scratch memory): a four-level select tree.
+__device__ __forceinline__ float pick16(const float (&f)[16], int e) {
+  // all-ones masks from the bits of e, opaque to the compiler so that the selects are not
+  // folded back into an indexed access
+  u32 m[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    m[k] = 0u - (((u32)e >> k) & 1u);
+    asm volatile("" : "+v"(m[k]));
+  }
+  auto sel = [](u32 mk, float hi, float lo) {
+    return __uint_as_float((__float_as_uint(hi) & mk) | (__float_as_uint(lo) & ~mk));
+  };
+  float a[8], b[4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = sel(m[0], f[2 * j + 1], f[2 * j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b[j] = sel(m[1], a[2 * j + 1], a[2 * j]);
+  return sel(m[3], sel(m[2], b[3], b[2]), sel(m[2], b[1], b[0]));
 }
 
 // Eight consecutive mask bytes at p (one 8-byte store when aligned and whole).
@@ -414,60 +458,85 @@ __global__ __launch_bounds__(kSelThreads) void select_lds_kernel(const float* sr
   write_suffix(m, K, recent, irow, mrow, keep_v, drop_v);
 }
 
-// Rows longer than kLdsRowMax: sample bracket, one classifying pass, exact resolution among
-// the candidates. `scratch` holds K ints per row (the kept indices above the bracket); with
-// no scratch the kernel takes the radix passes over HBM directly.
+// Rows longer than kLdsRowMax (up to kBitRowMax): sample bracket, one classifying pass,
+// exact resolution among the candidates, indices from a bitmap of the kept keys.
+//
+// The classifying pass needs no workgroup barrier: every thread classifies its own chunks
+// of 16 keys, records their kept bits in an LDS bitmap (one 16-bit word per chunk), counts
+// them, and appends its candidates to the LDS pool at a slot its wave reserves with one LDS
+// atomic. Candidates land in no particular order; ties at the threshold are then broken by
+// index with a second radix select over the tied candidates' indices. The ascending kept
+// indices come from one ordered pass over the bitmap (a single block prefix sum). Rows the
+// bitmap cannot hold, and brackets that miss, take the radix passes over HBM.
 __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float* src, long long src_stride, int m,
                                                                     int K, int recent, long long* idx, int budget,
                                                                     unsigned char* mask, long long mask_stride,
-                                                                    int invert, int* scratch) {
+                                                                    int invert) {
   constexpr int ST = kSelThreads;
   constexpr int CH = 16;                       // keys per thread per classifying step
-  __shared__ u32 skeys[kSamples];
+  static_assert(kBitRowMax / 32 >= kSamples, "the bitmap's LDS also holds the sample");
+  __shared__ u32 work[kBitRowMax / 32];        // the sample, then the bitmap of kept keys
   __shared__ u32 hist[2048];
-  __shared__ u32 ckey[kCandMax];               // candidate keys; later the kept candidates' indices
-  __shared__ int cidx[kCandMax];
+  __shared__ u32 ckey[kCandMax];               // candidate keys
+  __shared__ int cidx[kCandMax];               // candidate indices
   __shared__ __attribute__((aligned(16))) int scan_tmp[kSelWaves];
   __shared__ SelShared sh;
   __shared__ BracketShared bsh;
-  const int tid = threadIdx.x;
+  __shared__ int n_cand_lds;
+  const int tid = threadIdx.x, lane = tid & 63;
   const long long row = blockIdx.x;
   const float* x = src + row * src_stride;
   long long* irow = idx ? idx + row * (long long)budget : nullptr;
   unsigned char* mrow = mask ? mask + row * mask_stride : nullptr;
-  int* srow = scratch ? scratch + row * (long long)K : nullptr;
   const unsigned char keep_v = invert ? 0 : 1, drop_v = invert ? 1 : 0;
   auto hbm_key = [&](int i) { return order_key(x[i]); };
 
-  bool bracketed = K > 0 && (srow != nullptr || irow == nullptr);
+  bool bracketed = K > 0 && m <= kBitRowMax;
   int n_def = 0, n_cand = 0;
+  u32 key_hi = 0u, key_lo = 0u;                // the bracket
   if (bracketed) {
-    // ---- sample: thread t reads keys 4(t%2) .. +3 of segment t/2. Short segments keep the
-    // sample close to uniform: a dense run of large scores (the recent tokens of an
-    // importance row) then takes no more of the sample than of the row
-    {
-      const int seg = tid >> 1, off = (tid & 1) * 4;
-      const long long start = (long long)seg * (m - kSegLen) / (kSegs - 1);
+    if (tid == 0) n_cand_lds = 0;
+    auto bracket = [&]() __attribute__((always_inline)) {
+      // ---- sample: thread t reads keys 4(t%2) .. +3 of segment t/2. Short segments keep the
+      // sample close to uniform: a dense run of large scores (the recent tokens of an
+      // importance row) then takes no more of the sample than of the row
+      {
+        const int seg = tid >> 1, off = (tid & 1) * 4;
+        const long long start = (long long)seg * (m - kSegLen) / (kSegs - 1);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) skeys[4 * tid + e] = order_key(x[start + off + e]);
-    }
-    lds_barrier();
-    // ---- bracket: T is expected at sample rank r = K * kSamples / m; take ranks r -+ d,
-    // d = 4 sqrt(r + 1) + 8 (about four standard deviations of the sample rank)
-    int k_hi, k_lo;
-    bool has_hi, has_lo;
-    bracket_ranks(K, m, k_hi, k_lo, has_hi, has_lo);
-    u32 key_hi, key_lo;
-    auto s_key = [&](int i) { return skeys[i]; };
-    sample_bracket(s_key, k_hi, k_lo, has_hi, has_lo, hist, scan_tmp, &bsh, key_hi, key_lo);
+        for (int e = 0; e < 4; ++e) work[4 * tid + e] = order_key(x[start + off + e]);
+      }
+      lds_barrier();
+      // ---- bracket: T is expected at sample rank r = K * kSamples / m; take ranks r -+ d,
+      // d = 4 sqrt(r + 1) + 8 (about four standard deviations of the sample rank)
+      int k_hi, k_lo;
+      bool has_hi, has_lo;
+      bracket_ranks(K, m, k_hi, k_lo, has_hi, has_lo);
+      auto s_key = [&](int i) { return work[i]; };
+      sample_bracket(s_key, k_hi, k_lo, has_hi, has_lo, hist, scan_tmp, &bsh, key_hi, key_lo);
+    };
+    // the kept-key bitmap shares `work` with the sample, which bracket() consumes first
+    unsigned short* bits16 = (unsigned short*)work;
 
     // ---- classify every key once: above the bracket kept, below dropped, inside a candidate.
     // Two chunks ahead of the one being classified are in flight (16-byte loads, 128 bytes
-    // per thread, 128 KiB per workgroup) across the classification and its prefix sum. No
-    // load sits under a branch, per-lane or uniform: the compiler waits for a load at the end
-    // of the branch around it, which would serialise the prefetch. So the aligned and
-    // unaligned rows run separate instances of the loop, and a fetch past the end of the row
-    // rereads its first keys (a valid address), which are then ignored.
+    // per thread, 128 KiB per workgroup). No load sits under a branch, per-lane or uniform:
+    // the compiler waits for a load at the end of the branch around it, which would
+    // serialise the prefetch. So the aligned and unaligned rows run separate instances of
+    // the loop, and a fetch past the end of the row rereads its first keys (a valid
+    // address), which are then ignored.
+    int n_keep = 0;                               // this thread's kept keys
+    // Classification by float compares against the bracket: kept iff key > key_hi, i.e.
+    // v >= g_hi with g_hi = key_float(key_hi + 1), or v NaN while the bracket is bounded
+    // above; candidate iff key_lo <= key <= key_hi, i.e. v >= g_lo and not kept, or v NaN
+    // with the bracket open above (NaN's key is the largest).
+    bool nan_kept = false;
+    float g_hi = 0.f, g_lo = 0.f;
+    auto thresholds = [&]() __attribute__((always_inline)) {
+      nan_kept = key_hi != 0xffffffffu;
+      g_hi = nan_kept ? key_float(key_hi + 1u) : __builtin_nanf("");
+      g_lo = key_lo <= 0x007fffffu ? -__builtin_huge_valf() : key_float(key_lo);
+    };
     constexpr int STEP = ST * CH;
     auto classify_row = [&](auto aligned) __attribute__((always_inline)) {
       constexpr bool VEC = decltype(aligned)::value;
@@ -500,28 +569,31 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
         u32 kept = 0u, cand = 0u;
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
-          const u32 key = order_key(f[e]);
-          const bool valid = i0 + e < m;
-          kept |= (valid && key > key_hi ? 1u : 0u) << e;
-          cand |= (valid && key <= key_hi && key >= key_lo ? 1u : 0u) << e;
+          const float v = f[e];
+          const bool nan = v != v;
+          const bool ge_hi = v >= g_hi;
+          kept |= ((nan && nan_kept) || ge_hi ? 1u : 0u) << e;
+          cand |= ((nan && !nan_kept) || (v >= g_lo && !ge_hi) ? 1u : 0u) << e;
         }
-        int tot;
-        const int pre = block_exclusive_scan(__builtin_popcount(kept) | (__builtin_popcount(cand) << 16), scan_tmp,
-                                             tot);   // per chunk: <= 16384 each
-        // most chunks hold no kept or candidate key in a whole wave: skip the scatter there
-        if (__any((kept | cand) != 0u)) {
-          int pd = n_def + (pre & 0xffff), pc = n_cand + (pre >> 16);
-#pragma unroll
-          for (int e = 0; e < CH; ++e) {
-            if ((kept >> e) & 1u) {
-              if (srow && pd < K) srow[pd] = i0 + e;
-              ++pd;
-            } else if ((cand >> e) & 1u) {
-              if (pc < kCandMax) {
-                ckey[pc] = order_key(f[e]);
-                cidx[pc] = i0 + e;
-              }
-              ++pc;
+        const int nv = m - i0;                 // keys of this chunk inside the row
+        const u32 vmask = nv >= CH ? 0xffffu : (nv > 0 ? (1u << nv) - 1u : 0u);
+        kept &= vmask;
+        cand &= vmask;
+        if (i0 < m) bits16[i0 >> 4] = (unsigned short)kept;
+        n_keep += __builtin_popcount(kept);
+        // candidates: a slot range per wave from one LDS atomic; most chunks of a wave hold none
+        const int nc = __builtin_popcount(cand);
+        if (__any(nc != 0)) {
+          const int incl = wave_inclusive_scan(nc);
+          int base = 0;
+          if (lane == 63) base = atomicAdd(&n_cand_lds, incl);
+          int pc = __builtin_amdgcn_readlane(base, 63) + incl - nc;
+          // a lane holds few candidates: visit its set bits only
+          for (u32 c = cand; c != 0u; c &= c - 1u, ++pc) {
+            const int e = __builtin_ctz(c);
+            if (pc < kCandMax) {
+              ckey[pc] = order_key(pick16(f, e));
+              cidx[pc] = i0 + e;
             }
           }
         }
@@ -541,11 +613,12 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
             }
           }
         }
-        n_def += tot & 0xffff;
-        n_cand += tot >> 16;
       };
+      // the first two chunks' loads are in flight while the sample is read and bracketed
       fetch(buf0, 0);
       fetch(buf1, STEP);
+      bracket();
+      thresholds();
       for (int c0 = 0; c0 < m; c0 += 2 * STEP) {
         classify(buf0, c0);
         if (c0 + STEP < m) classify(buf1, c0 + STEP);
@@ -555,6 +628,10 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
       classify_row(std::true_type{});
     else
       classify_row(std::false_type{});
+    // full barrier: the pass's mask stores must be complete before candidates rewrite bytes
+    __syncthreads();
+    block_exclusive_scan(n_keep, scan_tmp, n_def);
+    n_cand = n_cand_lds;
     bracketed = n_def <= K && n_def + n_cand >= K && n_cand <= kCandMax;
   }
 
@@ -567,60 +644,53 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
     radix_select(hbm_key, m, K, 0u, 0xffffffffu, hist, scan_tmp, &sh, T, need, eq);
     ordered_output(hbm_key, m, K, T, need, eq == need, irow, mrow, keep_v, drop_v, scan_tmp);
   } else if (K > 0) {
-    __syncthreads();                           // candidates, scratch and mask of the pass are complete
     const int K2 = K - n_def;                  // candidates still to keep
-    int n_sel = 0;
     if (K2 > 0) {
-      u32 T;
+      u32 T, T2 = 0u;
       int need, eq;
       auto c_key = [&](int j) { return ckey[j]; };
-      radix_select(c_key, n_cand, K2, 0u, 0xffffffffu, hist, scan_tmp, &sh, T, need, eq);
+      radix_select(c_key, n_cand, K2, key_lo, key_hi, hist, scan_tmp, &sh, T, need, eq, true);
       const bool all_eq = eq == need;
-      int eq_base = 0;
-      for (int j0 = 0; j0 < n_cand; j0 += ST) {
-        const int j = j0 + tid;
-        const bool valid = j < n_cand;
-        const u32 key = valid ? ckey[j] : 0u;
-        const int ci = valid ? cidx[j] : 0;
-        const bool is_eq = valid && key == T;
-        int tie = 0;
-        if (!all_eq) {
-          int tot;
-          tie = block_exclusive_scan(is_eq ? 1 : 0, scan_tmp, tot) + eq_base;
-          eq_base += tot;
-        }
-        const bool sel = valid && (key > T || (is_eq && (all_eq || tie < need)));
-        int tot2;
-        const int rank = block_exclusive_scan(sel ? 1 : 0, scan_tmp, tot2) + n_sel;
-        n_sel += tot2;
-        if (sel) {
-          ckey[rank] = (u32)ci;                // ranks never pass a slot still to be read
+      if (!all_eq) {
+        // ties at T: the `need` lowest indices among them, i.e. the largest ~index
+        auto tie_key = [&](int j) { return ckey[j] == T ? ~(u32)cidx[j] : 0u; };
+        int need2, eq2;
+        radix_select(tie_key, n_cand, need, 0u, 0xffffffffu, hist, scan_tmp, &sh, T2, need2, eq2);
+      }
+      u32* bits = work;
+      for (int j = tid; j < n_cand; j += ST) {
+        const u32 key = ckey[j];
+        const int ci = cidx[j];
+        if (key > T || (key == T && (all_eq || ~(u32)ci >= T2))) {
+          atomicOr(&bits[ci >> 5], 1u << (ci & 31));
           if (mrow) mrow[ci] = keep_v;
         }
       }
       lds_barrier();
     }
     if (irow) {
-      // merge the two ascending lists: kept keys above the bracket (scratch, n_def) and kept
-      // candidates (ckey as indices, n_sel); an entry's slot is its rank in its own list plus
-      // the number of entries of the other list with a lower index
-      for (int a = tid; a < n_def; a += ST) {
-        const int v = srow[a];
-        int lo = 0, hi = n_sel;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if ((int)ckey[mid] < v) lo = mid + 1; else hi = mid;
+      // ascending kept indices: thread t owns bitmap words [t*wpt, (t+1)*wpt)
+      const u32* bits = work;
+      const int words = (m + 31) >> 5;
+      const int wpt = (words + ST - 1) / ST;
+      const int w0 = tid * wpt, w1 = min(words, w0 + wpt);
+      auto word = [&](int w) -> u32 {
+        const u32 v = bits[w];
+        const int valid = m - 32 * w;          // the last word's bits past m are not written
+        return valid >= 32 ? v : (v & ((1u << valid) - 1u));
+      };
+      int cnt = 0;
+      for (int w = w0; w < w1; ++w) cnt += __builtin_popcount(word(w));
+      int total;
+      int pos = block_exclusive_scan(cnt, scan_tmp, total);
+      for (int w = w0; w < w1; ++w) {
+        u32 v = word(w);
+        while (v) {
+          const int bit = __builtin_ctz(v);
+          if (pos < K) irow[pos] = 32 * w + bit;
+          ++pos;
+          v &= v - 1u;
         }
-        irow[a + lo] = v;
-      }
-      for (int j = tid; j < n_sel; j += ST) {
-        const int v = (int)ckey[j];
-        int lo = 0, hi = n_def;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (srow[mid] < v) lo = mid + 1; else hi = mid;
-        }
-        irow[j + lo] = v;
       }
     }
   }
@@ -697,10 +767,7 @@ using namespace fe;
 extern "C" size_t fe_select_workspace_bytes(int64_t rows, int64_t n, int64_t budget, int64_t recent,
                                             int pool_kernel) {
   if (rows <= 0 || n <= 0 || recent < 0 || recent > n || budget < recent || budget > n) return 0;
-  size_t bytes = pool_bytes(rows, n, budget, recent, pool_kernel);
-  // long rows: the kept indices above the sample bracket, K ints per row
-  if (n - recent > kLdsRowMax && budget > recent) bytes += (size_t)rows * (size_t)(budget - recent) * sizeof(int);
-  return bytes;
+  return pool_bytes(rows, n, budget, recent, pool_kernel);
 }
 
 extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t row_stride, int64_t budget,
@@ -741,14 +808,9 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
                        (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out, (long long)n,
                        invert ? 1 : 0);
   } else {
-    // scratch for the kept indices above the bracket; without room for it the kernel runs
-    // the radix passes over HBM instead
-    int* scratch = nullptr;
-    const size_t need = (size_t)rows * (size_t)K * sizeof(int);
-    if (K > 0 && workspace && workspace_bytes >= pbytes + need) scratch = (int*)((char*)workspace + pbytes);
     hipLaunchKernelGGL(select_sample_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, src, src_stride,
                        m, K, (int)recent, (long long*)indices_out, (int)budget, (unsigned char*)mask_out,
-                       (long long)n, invert ? 1 : 0, scratch);
+                       (long long)n, invert ? 1 : 0);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {

@@ -129,9 +129,7 @@ int fe_zero_f32(float* p, int64_t n, void* hip_stream);
  * indices_out: [rows, budget] int64, ascending. mask_out: [rows, n] bytes (0/1), the keep
  * mask, or the eviction mask (1 = evict) when invert != 0. Either output may be NULL.
  * workspace: device memory of at least fe_select_workspace_bytes(...) bytes (may be NULL
- * when that is 0): rows*(n-recent) floats of pooled scores when pooling, then, for rows
- * longer than 16384 past scores, rows*(budget-recent) ints for the kept indices of the
- * sampled schedule (without them the selection still completes, by radix passes over HBM).
+ * when that is 0): rows*(n-recent) floats of pooled scores when pooling, none otherwise.
  */
 size_t fe_select_workspace_bytes(int64_t rows, int64_t n, int64_t budget, int64_t recent,
                                  int pool_kernel);

@@ -99,9 +99,43 @@ def test_sampled_schedule_on_importance_like_rows(n, decay):
         _host_equal(x, budget, recent)
 
 
+@pytest.mark.parametrize("n", [70000, 131072])
+def test_sampled_schedule_ties_at_threshold(n):
+    """Quantised scores (about n/1000 equal keys per value): the bracket holds the threshold,
+    many candidates tie at it, and they are kept by index, lowest first."""
+    print(f"select ties at threshold n={n}", flush=True)
+    g = torch.Generator().manual_seed(n + 7)
+    x = (torch.rand((3, n), generator=g) * 1000).floor() / 1000
+    for budget, recent in ((1024, 64), (5000, 0), (333, 3)):
+        _host_equal(x, budget, recent)
+
+
+def test_sampled_schedule_denormals_and_zeros():
+    """Long rows whose threshold falls among FP32 denormals and signed zeros: the sampled
+    schedule classifies by float compares, which must order denormals and tie -0 with +0."""
+    print("select denormals and zeros", flush=True)
+    g = torch.Generator().manual_seed(21)
+    n = 40000
+    tiny = torch.tensor(1e-40, dtype=torch.float32)              # a denormal
+    x = (torch.randint(-200, 200, (4, n), generator=g).float() * tiny)
+    x[1, ::3] = -0.0
+    x[2] = torch.where(torch.rand((n,), generator=g) < 0.5, -tiny * 3, tiny * 3)
+    x[3, ::7] = float("nan")
+    for budget, recent in ((1024, 64), (20000, 0), (39999, 1)):
+        _host_equal(x, budget, recent)
+
+
+def test_rows_past_the_bitmap():
+    """Rows longer than the sampled schedule's kept-key bitmap (2^18 past scores) take the
+    radix passes over HBM."""
+    print("select rows past the bitmap", flush=True)
+    x = torch.rand((2, 300000), generator=torch.Generator().manual_seed(9))
+    _host_equal(x, 1024, 64)
+
+
 def test_sampled_schedule_fallbacks():
-    """Brackets that cannot hold the threshold (a large budget, heavy ties) and a call with no
-    room for the schedule's scratch take the radix passes over HBM: the same result."""
+    """Brackets that cannot hold the threshold (a large budget, heavy ties) take the radix
+    passes over HBM: the same result. Long rows need no workspace without pooling."""
     print("select fallbacks", flush=True)
     g = torch.Generator().manual_seed(3)
     x = torch.rand((2, 50000), generator=g)
@@ -113,8 +147,7 @@ def test_sampled_schedule_fallbacks():
     xd = x.cuda()
     idx = torch.empty((2, 1024), dtype=torch.int64, device="cuda")
     keep = torch.empty((2, 50000), dtype=torch.bool, device="cuda")
-    need = L.fe_select_workspace_bytes(2, 50000, 1024, 0, 1)     # rows past 16384 keys: scratch
-    assert need == 2 * 1024 * 4
+    assert L.fe_select_workspace_bytes(2, 50000, 1024, 0, 1) == 0
     _lib.check(L.fe_select(xd.data_ptr(), 2, 50000, 50000, 1024, 0, 1, idx.data_ptr(), keep.data_ptr(), 0,
                            None, 0, torch.cuda.current_stream().cuda_stream), "fe_select")
     hidx, hkeep = select_tokens(x, 1024)
