@@ -88,6 +88,29 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
   return x;
 }
 
+// Inclusive running minimum / maximum over the 64 lanes of a wave, the same DPP pattern as
+// wave_inclusive_scan (lanes without a source take the identity): lane 63 holds the wave's.
+__device__ __forceinline__ u32 wave_inclusive_min(u32 x) {
+  int v = (int)x;
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x111, 0xf, 0xf, false));
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x112, 0xf, 0xf, false));
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x114, 0xf, 0xf, false));
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x118, 0xf, 0xf, false));
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x142, 0xa, 0xf, false));
+  v = min((u32)v, (u32)__builtin_amdgcn_update_dpp(-1, v, 0x143, 0xc, 0xf, false));
+  return (u32)v;
+}
+__device__ __forceinline__ u32 wave_inclusive_max(u32 x) {
+  int v = (int)x;
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+  v = max((u32)v, (u32)__builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
+  return (u32)v;
+}
+
 // Exclusive prefix sum over the threads of a selection workgroup; `total` receives the sum.
 // tmp: kSelWaves ints, 16-byte aligned.
 __device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
@@ -119,11 +142,16 @@ struct SelShared {
 // (T undetermined) when the K-th largest key lies outside [lo, hi]; the full range
 // [0, 0xffffffff] always succeeds. With `within` (every key lies in [lo, hi]) the leading
 // digits that lo and hi share are known and their passes are skipped.
+//
+// Three LDS-only barriers per pass: after the histogram (whose successor, in the other half
+// of hist, is cleared meanwhile), after the per-wave sums of the bins each wave owns (every
+// thread then finds the wave holding the K-th key from 16 sums), and after the digit, found
+// by that wave alone, is published. hist: 2 x 2048 u32; tmp: 2 x kSelWaves ints.
 template <typename Get>
-__device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 hi, u32* hist, int* scan_tmp,
+__device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 hi, u32* hist, int* tmp,
                                              SelShared* sh, u32& T, int& need, int& eq, bool within = false) {
   constexpr int ST = kSelThreads;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   u32 prefix = 0, pmask = 0, eq_total = 0;
   int kk = K;
   int first = 0;
@@ -136,49 +164,78 @@ __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 
     }
     prefix = lo & pmask;
   }
+  for (int i = tid; i < (first == 2 ? 1024 : 2048); i += ST) hist[(first & 1) * 2048 + i] = 0u;
+  lds_barrier();
   for (int pass = first; pass < 3; ++pass) {
     const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
     const int nb = pass == 2 ? 1024 : 2048;
-    for (int i = tid; i < nb; i += ST) hist[i] = 0u;
-    lds_barrier();
+    u32* h = hist + (pass & 1) * 2048;
+    if (pass < 2) {
+      // the next pass's histogram: its last reader finished before this pass began
+      u32* hn = hist + ((pass + 1) & 1) * 2048;
+      for (int i = tid; i < (pass + 1 == 2 ? 1024 : 2048); i += ST) hn[i] = 0u;
+    }
     int above = 0;
 #pragma unroll 8
     for (int i = tid; i < n; i += ST) {
       const u32 key = get(i);
-      above += key > hi ? 1 : 0;
-      if (key >= lo && key <= hi && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & (u32)(nb - 1)], 1u);
+      if (pass == first) above += key > hi ? 1 : 0;
+      if (key >= lo && key <= hi && (key & pmask) == prefix) atomicAdd(&h[(key >> shift) & (u32)(nb - 1)], 1u);
     }
-    if (pass == 0) {
-      int n_above;
-      block_exclusive_scan(above, scan_tmp, n_above);
-      kk = K - n_above;
-    } else {
-      lds_barrier();
+    lds_barrier();
+    // wave w owns bins [nb - (w+1)*bpw, nb - w*bpw), lane l the bpl of them below
+    // nb - 1 - w*bpw - l*bpl: wave 0, lane 0 hold the highest digits
+    const int bpw = nb / kSelWaves, bpl = bpw / 64;
+    const int top = nb - 1 - w * bpw - lane * bpl;
+    int lsum = 0;
+    for (int e = 0; e < bpl; ++e) lsum += (int)h[top - e];
+    const int incl = wave_inclusive_scan(lsum);
+    const int wa = pass == first ? wave_inclusive_scan(above) : 0;
+    if (lane == 63) {
+      tmp[w] = incl;
+      tmp[kSelWaves + w] = wa;
     }
-    // thread t owns bins [nb - (t+1)*bpt, nb - t*bpt): thread 0 holds the highest digits
-    const int bpt = nb / ST;
-    const int hi_bin = nb - 1 - tid * bpt;
-    int local = 0;
-    for (int e = 0; e < bpt; ++e) local += (int)hist[hi_bin - e];
-    int total;
-    int cum = block_exclusive_scan(local, scan_tmp, total);
+    lds_barrier();
+    int total = 0, n_above = 0, cw = -1, before = 0;
+#pragma unroll
+    for (int i = 0; i < kSelWaves; ++i) {
+      total += tmp[i];
+      n_above += pass == first ? tmp[kSelWaves + i] : 0;
+    }
+    if (pass == first) kk = K - n_above;
     if (pass == 0 && (kk < 1 || kk > total)) return false;   // uniform: block totals
-    for (int e = 0; e < bpt; ++e) {
-      const int bin = hi_bin - e;
-      const int h = (int)hist[bin];
-      if (cum < kk && cum + h >= kk) {
-        sh->prefix = prefix | ((u32)bin << shift);
-        sh->kk = kk - cum;
-        sh->eq = (u32)h;
+    {
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < kSelWaves; ++i) {
+        const int t = tmp[i];
+        if (cw < 0 && c + t >= kk) {
+          cw = i;
+          before = c;
+        }
+        c += t;
       }
-      cum += h;
+    }
+    if (w == cw) {
+      int c = before + incl - lsum;            // keys in the bins above this lane's
+      if (c < kk && c + lsum >= kk) {
+        for (int e = 0; e < bpl; ++e) {
+          const int bin = top - e;
+          const int hv = (int)h[bin];
+          if (c < kk && c + hv >= kk) {
+            sh->prefix = prefix | ((u32)bin << shift);
+            sh->kk = kk - c;
+            sh->eq = (u32)hv;
+          }
+          c += hv;
+        }
+      }
     }
     lds_barrier();
     prefix = sh->prefix;
     kk = sh->kk;
     eq_total = sh->eq;
     pmask |= (u32)(nb - 1) << shift;
-    lds_barrier();
   }
   T = prefix;
   need = kk;
@@ -396,8 +453,8 @@ __global__ __launch_bounds__(kSelThreads) void select_lds_kernel(const float* sr
                                                                  int invert) {
   constexpr int ST = kSelThreads;
   __shared__ u32 keys[kLdsRowMax];
-  __shared__ u32 hist[2048];
-  __shared__ __attribute__((aligned(16))) int scan_tmp[kSelWaves];
+  __shared__ u32 hist[2 * 2048];
+  __shared__ __attribute__((aligned(16))) int scan_tmp[2 * kSelWaves];
   __shared__ SelShared sh;
   __shared__ BracketShared bsh;
   const int tid = threadIdx.x;
@@ -476,10 +533,10 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
   constexpr int CH = 16;                       // keys per thread per classifying step
   static_assert(kBitRowMax / 32 >= kSamples, "the bitmap's LDS also holds the sample");
   __shared__ u32 work[kBitRowMax / 32];        // the sample, then the bitmap of kept keys
-  __shared__ u32 hist[2048];
+  __shared__ u32 hist[2 * 2048];
   __shared__ u32 ckey[kCandMax];               // candidate keys
   __shared__ int cidx[kCandMax];               // candidate indices
-  __shared__ __attribute__((aligned(16))) int scan_tmp[kSelWaves];
+  __shared__ __attribute__((aligned(16))) int scan_tmp[2 * kSelWaves];
   __shared__ SelShared sh;
   __shared__ BracketShared bsh;
   __shared__ int n_cand_lds;
@@ -494,6 +551,7 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
   bool bracketed = K > 0 && m <= kBitRowMax;
   int n_def = 0, n_cand = 0;
   u32 key_hi = 0u, key_lo = 0u;                // the bracket
+  u32 c_lo = 0xffffffffu, c_hi = 0u;            // range of the candidate keys (per thread, then all)
   if (bracketed) {
     if (tid == 0) n_cand_lds = 0;
     auto bracket = [&]() __attribute__((always_inline)) {
@@ -592,7 +650,10 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
           for (u32 c = cand; c != 0u; c &= c - 1u, ++pc) {
             const int e = __builtin_ctz(c);
             if (pc < kCandMax) {
-              ckey[pc] = order_key(pick16(f, e));
+              const u32 ck = order_key(pick16(f, e));
+              ckey[pc] = ck;
+              c_lo = min(c_lo, ck);
+              c_hi = max(c_hi, ck);
               cidx[pc] = i0 + e;
             }
           }
@@ -630,7 +691,28 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
       classify_row(std::false_type{});
     // full barrier: the pass's mask stores must be complete before candidates rewrite bytes
     __syncthreads();
-    block_exclusive_scan(n_keep, scan_tmp, n_def);
+    {
+      // kept count, and the range of the candidate keys: the radix select below skips the
+      // digits all candidates share (with the bracket open above, the bracket's own ends
+      // share none, and a first pass would pile every candidate into one histogram bin)
+      const int w = tid >> 6;
+      const int x = wave_inclusive_scan(n_keep);
+      const u32 wlo = wave_inclusive_min(c_lo), whi = wave_inclusive_max(c_hi);
+      if (lane == 63) {
+        scan_tmp[w] = x;
+        scan_tmp[kSelWaves + w] = (int)wlo;
+        hist[w] = whi;                           // free until the radix select clears it
+      }
+      lds_barrier();
+      n_def = 0;
+#pragma unroll
+      for (int i = 0; i < kSelWaves; ++i) {
+        n_def += scan_tmp[i];
+        c_lo = min(c_lo, (u32)scan_tmp[kSelWaves + i]);
+        c_hi = max(c_hi, hist[i]);
+      }
+      lds_barrier();
+    }
     n_cand = n_cand_lds;
     bracketed = n_def <= K && n_def + n_cand >= K && n_cand <= kCandMax;
   }
@@ -649,7 +731,7 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
       u32 T, T2 = 0u;
       int need, eq;
       auto c_key = [&](int j) { return ckey[j]; };
-      radix_select(c_key, n_cand, K2, key_lo, key_hi, hist, scan_tmp, &sh, T, need, eq, true);
+      radix_select(c_key, n_cand, K2, c_lo, c_hi, hist, scan_tmp, &sh, T, need, eq, true);
       const bool all_eq = eq == need;
       if (!all_eq) {
         // ties at T: the `need` lowest indices among them, i.e. the largest ~index
