@@ -140,8 +140,8 @@ struct SelShared {
 // need = how many keys equal to T are among the K largest, eq = how many keys equal T.
 // Only keys in [lo, hi] are histogrammed; keys above hi are counted first. Returns false
 // (T undetermined) when the K-th largest key lies outside [lo, hi]; the full range
-// [0, 0xffffffff] always succeeds. With `within` (every key lies in [lo, hi]) the leading
-// digits that lo and hi share are known and their passes are skipped.
+// [0, 0xffffffff] always succeeds. The leading digits that lo and hi share are the same for
+// every key in [lo, hi], so their passes are skipped.
 //
 // Three LDS-only barriers per pass: after the histogram (whose successor, in the other half
 // of hist, is cleared meanwhile), after the per-wave sums of the bins each wave owns (every
@@ -149,13 +149,13 @@ struct SelShared {
 // by that wave alone, is published. hist: 2 x 2048 u32; tmp: 2 x kSelWaves ints.
 template <typename Get>
 __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 hi, u32* hist, int* tmp,
-                                             SelShared* sh, u32& T, int& need, int& eq, bool within = false) {
+                                             SelShared* sh, u32& T, int& need, int& eq) {
   constexpr int ST = kSelThreads;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   u32 prefix = 0, pmask = 0, eq_total = 0;
   int kk = K;
   int first = 0;
-  if (within && (lo >> 21) == (hi >> 21)) {
+  if ((lo >> 21) == (hi >> 21)) {
     first = 1;
     pmask = 0xffe00000u;
     if ((lo >> 10) == (hi >> 10)) {
@@ -203,7 +203,7 @@ __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 
       n_above += pass == first ? tmp[kSelWaves + i] : 0;
     }
     if (pass == first) kk = K - n_above;
-    if (pass == 0 && (kk < 1 || kk > total)) return false;   // uniform: block totals
+    if (pass == first && (kk < 1 || kk > total)) return false;   // uniform: block totals
     {
       int c = 0;
 #pragma unroll
@@ -244,11 +244,11 @@ __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 
 }
 
 // Bracket of a sample of kSamples keys (key i = get(i)): for sample ranks k_hi < k_lo
-// (1-based, from the top), the 22-bit prefixes of the k_hi-th and k_lo-th largest sample
-// keys, from a first radix pass shared by both ranks and a second pass per rank. key_hi is
-// the largest key with the first prefix (keys above it rank above T with high
-// probability), key_lo the smallest key with the second; without a rank the bracket is
-// open on that side.
+// (1-based, from the top), the prefixes of the k_hi-th and k_lo-th largest sample keys
+// down to 22 bits below the prefix all samples share, from a first radix pass shared by
+// both ranks and a second pass per rank. key_hi is the largest key with the first prefix
+// (keys above it rank above T with high probability), key_lo the smallest key with the
+// second; without a rank the bracket is open on that side.
 struct BracketShared {
   int bin[2], rest[2], sub[2];
 };
@@ -257,14 +257,40 @@ template <typename Get>
 __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool has_hi, bool has_lo, u32* hist,
                                                int* scan_tmp, BracketShared* sh, u32& key_hi, u32& key_lo) {
   constexpr int ST = kSelThreads;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int target[2] = {k_hi, k_lo};
   const bool live[2] = {has_hi, has_lo};
   const int hi_bin = 2047 - 2 * tid;            // thread t owns bins hi_bin, hi_bin - 1
-  // pass 1: top 11 bits
+  // The two 11-bit digits start right below the prefix all sample keys share (from their
+  // minimum and maximum): for scores spread over a few binades the top 11 bits hold little
+  // more than the exponent, and a histogram of them piles most samples into a few bins.
+  u32 smin = 0xffffffffu, smax = 0u;
+  for (int i = tid; i < kSamples; i += ST) {
+    const u32 k = get(i);
+    smin = min(smin, k);
+    smax = max(smax, k);
+  }
+  smin = wave_inclusive_min(smin);
+  smax = wave_inclusive_max(smax);
+  if (lane == 63) {
+    scan_tmp[w] = (int)smin;
+    scan_tmp[kSelWaves + w] = (int)smax;
+  }
   for (int i = tid; i < 2048; i += ST) hist[i] = 0u;
   lds_barrier();
-  for (int i = tid; i < kSamples; i += ST) atomicAdd(&hist[get(i) >> 21], 1u);
+#pragma unroll
+  for (int i = 0; i < kSelWaves; ++i) {
+    smin = min(smin, (u32)scan_tmp[i]);
+    smax = max(smax, (u32)scan_tmp[kSelWaves + i]);
+  }
+  const int plen = (smin ^ smax) ? __builtin_clz(smin ^ smax) : 32;   // shared leading bits
+  int s0 = 32 - plen - 11;                      // first digit: bits [s0, s0 + 11)
+  s0 = s0 < 11 ? 11 : (s0 > 21 ? 21 : s0);
+  const u32 pmask = s0 == 21 ? 0u : ~0u << (s0 + 11);
+  const u32 prefix = smin & pmask;
+  const int s1 = s0 - 11;                       // second digit: bits [s1, s0)
+  // pass 1: the first digit
+  for (int i = tid; i < kSamples; i += ST) atomicAdd(&hist[(get(i) >> s0) & 2047u], 1u);
   lds_barrier();
   int total;
   int cum = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
@@ -278,7 +304,7 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
     cum += h;
   }
   lds_barrier();
-  // pass 2, per rank: the next 11 bits of the sample keys in that rank's bin
+  // pass 2, per rank: the second digit of the sample keys in that rank's bin
   for (int t = 0; t < 2; ++t) {
     if (!live[t]) continue;
     const int b = sh->bin[t], r = sh->rest[t];
@@ -286,7 +312,7 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
     lds_barrier();
     for (int i = tid; i < kSamples; i += ST) {
       const u32 key = get(i);
-      if ((int)(key >> 21) == b) atomicAdd(&hist[(key >> 10) & 2047u], 1u);
+      if ((int)((key >> s0) & 2047u) == b) atomicAdd(&hist[(key >> s1) & 2047u], 1u);
     }
     lds_barrier();
     int c = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
@@ -297,8 +323,9 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
     }
     lds_barrier();
   }
-  key_hi = has_hi ? (((u32)sh->bin[0] << 21) | ((u32)sh->sub[0] << 10) | 0x3ffu) : 0xffffffffu;
-  key_lo = has_lo ? (((u32)sh->bin[1] << 21) | ((u32)sh->sub[1] << 10)) : 0u;
+  const u32 low = (1u << s1) - 1u;
+  key_hi = has_hi ? (prefix | ((u32)sh->bin[0] << s0) | ((u32)sh->sub[0] << s1) | low) : 0xffffffffu;
+  key_lo = has_lo ? (prefix | ((u32)sh->bin[1] << s0) | ((u32)sh->sub[1] << s1)) : 0u;
   lds_barrier();
 }
 
@@ -731,7 +758,7 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
       u32 T, T2 = 0u;
       int need, eq;
       auto c_key = [&](int j) { return ckey[j]; };
-      radix_select(c_key, n_cand, K2, c_lo, c_hi, hist, scan_tmp, &sh, T, need, eq, true);
+      radix_select(c_key, n_cand, K2, c_lo, c_hi, hist, scan_tmp, &sh, T, need, eq);
       const bool all_eq = eq == need;
       if (!all_eq) {
         // ties at T: the `need` lowest indices among them, i.e. the largest ~index
