@@ -246,21 +246,44 @@ __device__ __forceinline__ bool radix_select(Get get, int n, int K, u32 lo, u32 
 // Bracket of a sample of kSamples keys (key i = get(i)): for sample ranks k_hi < k_lo
 // (1-based, from the top), the prefixes of the k_hi-th and k_lo-th largest sample keys
 // down to 22 bits below the prefix all samples share, from a first radix pass shared by
-// both ranks and a second pass per rank. key_hi is the largest key with the first prefix
+// both ranks and a second pass that counts both ranks' bins at once (rank 0 in the low,
+// rank 1 in the high half of each 32-bit count; a sample holds at most 4096 keys, so the
+// halves never carry into each other). key_hi is the largest key with the first prefix
 // (keys above it rank above T with high probability), key_lo the smallest key with the
-// second; without a rank the bracket is open on that side.
+// second; without a rank the bracket is open on that side. Seven LDS barriers: the two
+// scans use opposite halves of scan_tmp, so neither needs a barrier after its reads.
 struct BracketShared {
   int bin[2], rest[2], sub[2];
 };
 
+// Exclusive block scan with one barrier: tmp (kSelWaves ints) must not be written again
+// before a later barrier.
+__device__ __forceinline__ int block_exclusive_scan_once(int v, int* tmp, int& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int x = wave_inclusive_scan(v);
+  if (lane == 63) tmp[w] = x;
+  lds_barrier();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < kSelWaves; ++i) {
+    const int t = tmp[i];
+    before += (i < w) ? t : 0;
+    total += t;
+  }
+  return before + x - v;
+}
+
 template <typename Get>
 __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool has_hi, bool has_lo, u32* hist,
                                                int* scan_tmp, BracketShared* sh, u32& key_hi, u32& key_lo) {
+  static_assert(kSamples < 65536, "packed second-pass counts");
   constexpr int ST = kSelThreads;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int target[2] = {k_hi, k_lo};
   const bool live[2] = {has_hi, has_lo};
   const int hi_bin = 2047 - 2 * tid;            // thread t owns bins hi_bin, hi_bin - 1
+  u32* hist2 = hist + 2048;                     // second pass, both ranks packed
   // The two 11-bit digits start right below the prefix all sample keys share (from their
   // minimum and maximum): for scores spread over a few binades the top 11 bits hold little
   // more than the exponent, and a histogram of them piles most samples into a few bins.
@@ -276,8 +299,8 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
     scan_tmp[w] = (int)smin;
     scan_tmp[kSelWaves + w] = (int)smax;
   }
-  for (int i = tid; i < 2048; i += ST) hist[i] = 0u;
-  lds_barrier();
+  for (int i = tid; i < 2 * 2048; i += ST) hist[i] = 0u;
+  lds_barrier();                                                      // 1
 #pragma unroll
   for (int i = 0; i < kSelWaves; ++i) {
     smin = min(smin, (u32)scan_tmp[i]);
@@ -291,9 +314,10 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
   const int s1 = s0 - 11;                       // second digit: bits [s1, s0)
   // pass 1: the first digit
   for (int i = tid; i < kSamples; i += ST) atomicAdd(&hist[(get(i) >> s0) & 2047u], 1u);
-  lds_barrier();
+  lds_barrier();                                                      // 2
   int total;
-  int cum = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
+  // scan_tmp[0, kSelWaves) was last read before barrier 2
+  int cum = block_exclusive_scan_once((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);   // 3
   for (int e = 0; e < 2; ++e) {
     const int bin = hi_bin - e, h = (int)hist[bin];
     for (int t = 0; t < 2; ++t)
@@ -303,30 +327,30 @@ __device__ __forceinline__ void sample_bracket(Get get, int k_hi, int k_lo, bool
       }
     cum += h;
   }
-  lds_barrier();
-  // pass 2, per rank: the second digit of the sample keys in that rank's bin
-  for (int t = 0; t < 2; ++t) {
-    if (!live[t]) continue;
-    const int b = sh->bin[t], r = sh->rest[t];
-    for (int i = tid; i < 2048; i += ST) hist[i] = 0u;
-    lds_barrier();
-    for (int i = tid; i < kSamples; i += ST) {
-      const u32 key = get(i);
-      if ((int)((key >> s0) & 2047u) == b) atomicAdd(&hist[(key >> s1) & 2047u], 1u);
-    }
-    lds_barrier();
-    int c = block_exclusive_scan((int)(hist[hi_bin] + hist[hi_bin - 1]), scan_tmp, total);
-    for (int e = 0; e < 2; ++e) {
-      const int bin = hi_bin - e, h = (int)hist[bin];
-      if (c < r && c + h >= r) sh->sub[t] = bin;
-      c += h;
-    }
-    lds_barrier();
+  lds_barrier();                                                      // 4
+  // pass 2: the second digit of the sample keys in either rank's bin
+  const int b0 = live[0] ? sh->bin[0] : -1, b1 = live[1] ? sh->bin[1] : -1;
+  for (int i = tid; i < kSamples; i += ST) {
+    const u32 key = get(i);
+    const int d = (int)((key >> s0) & 2047u);
+    const u32 add = (d == b0 ? 1u : 0u) + (d == b1 ? 65536u : 0u);
+    if (add) atomicAdd(&hist2[(key >> s1) & 2047u], add);
   }
+  lds_barrier();                                                      // 5
+  // scan_tmp[kSelWaves, 2 kSelWaves) was last read before barrier 2
+  int c = block_exclusive_scan_once((int)(hist2[hi_bin] + hist2[hi_bin - 1]), scan_tmp + kSelWaves, total);   // 6
+  const int r0 = live[0] ? sh->rest[0] : 0, r1 = live[1] ? sh->rest[1] : 0;
+  for (int e = 0; e < 2; ++e) {
+    const int bin = hi_bin - e, h = (int)hist2[bin];
+    const int c0 = c & 0xffff, h0 = h & 0xffff, c1 = (int)((u32)c >> 16), h1 = (int)((u32)h >> 16);
+    if (c0 < r0 && c0 + h0 >= r0) sh->sub[0] = bin;
+    if (c1 < r1 && c1 + h1 >= r1) sh->sub[1] = bin;
+    c += h;
+  }
+  lds_barrier();                                                      // 7
   const u32 low = (1u << s1) - 1u;
   key_hi = has_hi ? (prefix | ((u32)sh->bin[0] << s0) | ((u32)sh->sub[0] << s1) | low) : 0xffffffffu;
   key_lo = has_lo ? (prefix | ((u32)sh->bin[1] << s0) | ((u32)sh->sub[1] << s1)) : 0u;
-  lds_barrier();
 }
 
 // Sample ranks bracketing the K-th largest of m keys: T is expected at rank
@@ -581,16 +605,24 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
   u32 c_lo = 0xffffffffu, c_hi = 0u;            // range of the candidate keys (per thread, then all)
   if (bracketed) {
     if (tid == 0) n_cand_lds = 0;
-    auto bracket = [&]() __attribute__((always_inline)) {
-      // ---- sample: thread t reads keys 4(t%2) .. +3 of segment t/2. Short segments keep the
-      // sample close to uniform: a dense run of large scores (the recent tokens of an
-      // importance row) then takes no more of the sample than of the row
-      {
-        const int seg = tid >> 1, off = (tid & 1) * 4;
-        const long long start = (long long)seg * (m - kSegLen) / (kSegs - 1);
+    // ---- sample: thread t reads keys 4(t%2) .. +3 of segment t/2. Short segments keep the
+    // sample close to uniform: a dense run of large scores (the recent tokens of an
+    // importance row) then takes no more of the sample than of the row. The loads are
+    // issued before the streaming pass's first chunks, so they do not queue behind them.
+    float sv[4];
+    auto sample_load = [&]() __attribute__((always_inline)) {
+      const int seg = tid >> 1, off = (tid & 1) * 4;
+      const long long start = (long long)seg * (m - kSegLen) / (kSegs - 1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) work[4 * tid + e] = order_key(x[start + off + e]);
-      }
+      for (int e = 0; e < 4; ++e) sv[e] = x[start + off + e];
+    };
+    auto bracket = [&]() __attribute__((always_inline)) {
+      // opaque to the compiler: it would otherwise hoist the first use of the sample (part
+      // of order_key) above the branch between the aligned and unaligned loops, waiting
+      // for the sample before the streaming pass's loads are issued
+      asm volatile("" : "+v"(sv[0]), "+v"(sv[1]), "+v"(sv[2]), "+v"(sv[3]));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) work[4 * tid + e] = order_key(sv[e]);
       lds_barrier();
       // ---- bracket: T is expected at sample rank r = K * kSamples / m; take ranks r -+ d,
       // d = 4 sqrt(r + 1) + 8 (about four standard deviations of the sample rank)
@@ -702,7 +734,8 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
           }
         }
       };
-      // the first two chunks' loads are in flight while the sample is read and bracketed
+      // the first two chunks' loads are in flight while the sample is bracketed
+      sample_load();
       fetch(buf0, 0);
       fetch(buf1, STEP);
       bracket();
