@@ -553,10 +553,19 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 // this traversal needs far fewer registers than traversal 1. A workgroup holds 8 row tiles
 // that share every K tile (one FP32 atomic per key and tile per workgroup), as 8/TPW waves
 // of TPW row tiles each. TPW = 1 runs at four waves per SIMD. TPW = 2 (the default) runs at
-// three (three workgroups per CU; 168 registers with a few values spilled, 1.5% faster than
-// at two), with every K fragment read from LDS feeding two MFMAs: that halves the LDS read
+// three (three workgroups per CU; 168 registers, none spilled, 1.5% faster than at two),
+// with every K fragment read from LDS feeding two MFMAs: that halves the LDS read
 // traffic, the co-bottleneck of this traversal next to the MFMAs, and measures about 3%
 // faster than TPW = 1. The K tiles use the attention kernel's channel-group-major layout.
+// The lane's index, recomputed where it is used: opaque to the compiler, which would
+// otherwise keep values derived from it live across the replay's tile loop and, at three
+// waves per SIMD, spill them (each reload then waits behind the next tile's DMA).
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 template <typename E, int DP, int TPW>
 __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
@@ -628,12 +637,13 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
   float* imp_row = a.imp + (long long)bh * N;
 
   auto flush = [&](int kb_prev, int buf_prev) {
-    if (tid < BN) {
-      const float* rr = red + buf_prev * NW * BN + tid;
+    if (wv == 0) {                               // BN = 64: wave 0 sums one key per lane
+      const int ln = lane_now();
+      const float* rr = red + buf_prev * NW * BN + ln;
       float sum = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
-      const int key = kb_prev + tid;
+      const int key = kb_prev + ln;
       if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
     }
   };
@@ -663,7 +673,8 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
         for (int j = 0; j < TPW; ++j) {
           // lanes hold key kb + 32s + l32; causal mask on diagonal tiles
           if (a.causal && kb + BN - 1 > q0[j]) {
-            const int rel = kb + 32 * s + l32 - q0[j] - 4 * hh;
+            const int ln = lane_now();
+            const int rel = (ln & 31) - 4 * (ln >> 5) + (kb + 32 * s - q0[j]);
 #pragma unroll
             for (int i = 0; i < 16; ++i) sacc[j][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[j][i];
           }
@@ -681,10 +692,11 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
     }
     cs[0] = half_swap_sum(cs[0]);
     cs[1] = half_swap_sum(cs[1]);
-    if (hh == 0) {
+    const int ln = lane_now();
+    if (ln < 32) {
       float* rb = red + BUF * NW * BN + wv * BN;
-      rb[l32] = cs[0];
-      rb[32 + l32] = cs[1];
+      rb[ln] = cs[0];
+      rb[32 + ln] = cs[1];
     }
   };
 
