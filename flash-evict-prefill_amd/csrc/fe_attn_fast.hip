@@ -151,13 +151,16 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
   const int lo_lim = !tv ? -1 : (a.causal ? min(q0, N - 1) : N - 1);
   const int wave_hi = !tv ? -1 : (a.causal ? min(q0 + 31, N - 1) : N - 1);
 
+  // A negative scale runs as |scale| on -Q: the sign bits of Q flip at load, and
+  // (-q).k = -(q.k) exactly in the FP32 accumulation, so the logits are those of scale * Q K^T
+  const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
   u32x4 qf[NDC];
   {
     const int qr = q0 + l32;
     const bool ok = tv && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
   }
 
   // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 #pragma unroll
       for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
     }
-    return half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15]))) * a.scale_log2;
+    return half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15]))) * a.abs_scale_log2;
   };
   // S^T of one tile into sacc, masked on diagonal and ragged tiles
   auto qk_tile = [&](int kb, int BUF, int SLOT, f32x16(&sacc)[2]) __attribute__((always_inline)) {
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
       float p[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        p[i] = fast_exp2(fmaf(sacc[s][i], a.scale_log2, nm));
+        p[i] = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nm));
         if constexpr (EXACT) ps[i & 3] = s == 0 && i < 4 ? p[i] : ps[i & 3] + p[i];
       }
 #pragma unroll
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
           float c4[4];
   #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float e = fast_exp2(fmaf(sacc[s][i], a.scale_log2, nb[i]));
+            const float e = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nb[i]));
             if (i < 4)
               c4[i] = e;
             else
@@ -605,6 +608,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
   // This wave's row tiles j: 32 query positions from q0[j] of query head head[j]. A operand:
   // query row q0 + l32, channels 16c + 8h .. +7; nb: minus the bias of the 16 rows a lane
   // holds in the accumulator (register i: row 8(i/4) + 4h + i%4).
+  const u32 qneg = a.neg_scale ? 0x80008000u : 0u;   // a negative scale runs as |scale| on -Q
   int q0[TPW];
   u32x4 qf[TPW][NDC];
   float nb[TPW][16];
@@ -622,7 +626,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
     const bool ok = rin && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? *(const u32x4*)(qp + 16 * c + 8 * hh) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     const float br = ok ? a.bias[(long long)(b * a.Hq + head) * N + qr] : POS_INF;
 #pragma unroll
     for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
@@ -680,7 +684,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
           }
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float e = fast_exp2(fmaf(sacc[j][i], a.scale_log2, nb[j][i]));
+            const float e = fast_exp2(fmaf(sacc[j][i], a.abs_scale_log2, nb[j][i]));
             if (j == 0 && i < 4)
               c4[i] = e;
             else
@@ -758,7 +762,10 @@ bool kv_ok(const void* p, const long long* st, int N, int D) {
 
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   if (a.D != 64 && a.D != 128) return false;
-  if (!(a.scale_log2 > 0.f) || !a.qvec) return false;
+  // Q is read once per row tile, element-wise when it is not 16-byte vectorisable (any
+  // strides); K and V go through the tile DMA, which needs aligned unit-stride rows. A zero
+  // scale takes the generic kernel.
+  if (!(a.abs_scale_log2 > 0.f)) return false;
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
   const bool fused = a.score && !a.bias;
   const int idx = 2 * ((dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0)) + (fused ? 1 : 0);

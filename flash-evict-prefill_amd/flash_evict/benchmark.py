@@ -25,6 +25,11 @@ Modes (q [1,H,N,D], k/v [1,Hkv,N,D] bf16):
   --kernels    the HBM-bound kernels on scaled synthetics (the headline's score array is
                only 1 MiB, where they are launch-latency bound): achieved GB/s of
                algorithmic bytes (each input byte read once, each output byte written once)
+  --generic    prefill on the shapes and layouts the gfx950 fast path does not take (head
+               dims other than 64/128, a zero scale, K/V rows off 16-byte alignment), next to
+               the fast path at D = 64 and 128 (and at D = 128 with a negative scale and with
+               a channel-strided q, which it reads element-wise): attention only, and with
+               every row replayed; TFLOP/s of the work the kernels execute
 
 Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
 --dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
@@ -357,6 +362,67 @@ def kernel_rows(repeats):
     return out
 
 
+# ---------------------------------------------------------------- generic attention path
+
+def _attention_flop(hq, n, d, replay):
+    """Causal attention FLOP of one layer (B = 1): QK^T and P@V over the n(n+1)/2 visible
+    pairs, plus the replay's QK^T recomputation when every row is replayed."""
+    pairs = n * (n + 1) // 2
+    return (4 + (2 if replay else 0)) * pairs * d * hq
+
+
+@torch.inference_mode()
+def generic_rows(repeats, n=8192, hq=32, hk=8):
+    """prefill() on the layouts of the generic kernel (fe_attn.hip) and of the fast path."""
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+
+    def inputs(d):
+        q = torch.randn((1, hq, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
+        k = torch.randn((1, hk, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
+        v = torch.randn((1, hk, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
+        return q, k, v
+
+    def strided_q(d):
+        q2 = torch.randn((1, hq, n, 2 * d), device="cuda", generator=g, dtype=torch.bfloat16)
+        _, k, v = inputs(d)
+        return q2[..., ::2], k, v                  # channel stride 2
+
+    def offset_kv(d):
+        q, _, _ = inputs(d)
+        size = hk * n * d
+        flat = torch.randn(2 * size + 1, device="cuda", generator=g, dtype=torch.bfloat16)
+        k = flat[1:1 + size].view(1, hk, n, d)      # rows 2 bytes off 16-byte alignment
+        v = flat[1 + size:1 + 2 * size].view(1, hk, n, d)
+        return q, k, v
+
+    cases = [("fast D=128", "fast", 128, lambda: inputs(128), None),
+             ("fast D=64", "fast", 64, lambda: inputs(64), None),
+             ("generic D=32", "generic", 32, lambda: inputs(32), None),
+             ("generic D=96", "generic", 96, lambda: inputs(96), None),
+             ("generic D=256", "generic", 256, lambda: inputs(256), None),
+             ("fast D=128 negative scale", "fast", 128, lambda: inputs(128), -(128 ** -0.5)),
+             ("generic D=128 zero scale", "generic", 128, lambda: inputs(128), 0.0),
+             ("fast D=128 q channel stride 2", "fast", 128, lambda: strided_q(128), None),
+             ("generic D=128 K/V rows misaligned", "generic", 128, lambda: offset_kv(128), None)]
+    out = []
+    for name, path, d, make, scale in cases:
+        q, k, v = make()
+        for replay in (False, True):
+            fn = (lambda: prefill(q, k, v, scale=scale, recency_decay=0.0)) if replay else \
+                 (lambda: prefill(q, k, v, scale=scale, score=False))
+            # ten warm-ups: the part runs the first launches of a fast-path case at a higher
+            # clock than it holds once its power draw has built up
+            ms = statistics.median(event_samples(fn, repeats, warmup=10))
+            flop = _attention_flop(hq, n, d, replay)
+            out.append({"case": name, "path": path, "work": "attention + full replay" if replay else "attention only",
+                        "shape": "B1 Hq%d Hkv%d N%d D%d bf16 causal" % (hq, hk, n, d), "median_ms": ms,
+                        "executed_tflop": flop / 1e12, "TFLOP/s": flop / (ms * 1e-3) / 1e12,
+                        "frac_of_2.5PFLOP/s": flop / (ms * 1e-3) / 2.5e15})
+            print(json.dumps(out[-1]), flush=True)
+        del q, k, v
+    return out
+
+
 # ---------------------------------------------------------------- command line
 
 def main(argv=None):
@@ -370,14 +436,15 @@ def main(argv=None):
     p.add_argument("--output", default="benchmark.json")
     p.add_argument("--require-idle", action="store_true", help="refuse rows measured while another process holds the GPU")
     p.add_argument("--kernels", action="store_true", help="time the HBM-bound kernels on scaled synthetics")
+    p.add_argument("--generic", action="store_true", help="prefill on the generic kernel's shapes and layouts")
     p.add_argument("--policies", action="store_true", help="policy latency at fixed budgets")
     p.add_argument("--budgets", type=int, nargs="+", default=[256, 1024])
     p.add_argument("--policy-file", default=None, help="JSON list of scoring policies (--policies)")
     args = p.parse_args(argv)
 
-    if args.kernels:
+    if args.kernels or args.generic:
         data = {"gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "hip": torch.version.hip,
-                "rows": kernel_rows(args.repeats)}
+                "rows": kernel_rows(args.repeats) if args.kernels else generic_rows(args.repeats)}
         Path(args.output).write_text(json.dumps(data, indent=2) + "\n")
         return
 

@@ -55,9 +55,11 @@ def test_generic_head_dims(d):
     torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("scale", [-0.1, 0.0, 0.5, 3.0])
-def test_scales(scale):
-    q, k, v = _qkv(n=130, d=64, seed=11)
+def test_scales(scale, d):
+    # D = 64/128: a negative scale runs on the fast kernels (|scale| on -Q), zero on the generic one
+    q, k, v = _qkv(n=130, d=d, seed=11)
     for causal in (True, False):
         out, imp = prefill(q, k, v, scale=scale, causal=causal)
         ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), scale=scale, causal=causal)
@@ -84,6 +86,28 @@ def test_unusual_layouts():
     ref_out, ref_imp = materialized(q.cpu(), k0.cpu(), k0.cpu())
     torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
     torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_strided_q_on_the_fast_path(d):
+    # Q with channel stride 2, or 2 bytes off 16-byte alignment, and aligned K/V: the fast
+    # kernels read such a Q element-wise, so the result equals the contiguous call bit for bit
+    q, k, v = _qkv(hq=4, hk=2, n=200, d=d, seed=21)
+    wide = torch.zeros((1, 4, 200, 2 * d), dtype=q.dtype, device=q.device)
+    wide[..., ::2] = q
+    flat = torch.zeros(q.numel() + 1, dtype=q.dtype, device=q.device)
+    flat[1:] = q.reshape(-1)
+    for causal in (True, False):
+        ref_out, ref_imp = prefill(q, k, v, causal=causal, recency_decay=0.02)
+        for qq in (wide[..., ::2], flat[1:].view(q.shape)):
+            assert qq.stride(-1) != 1 or qq.data_ptr() % 16 != 0
+            out, imp = prefill(qq, k, v, causal=causal, recency_decay=0.02)
+            assert torch.equal(out, ref_out)
+            # same kernels; only the order of the FP32 atomic additions can differ
+            assert float((imp - ref_imp).abs().max()) <= 2e-6 * float(ref_imp.abs().max())
+        o_out, o_imp = materialized(q.cpu(), k.cpu(), v.cpu(), causal=causal, recency_decay=0.02)
+        torch.testing.assert_close(ref_out.float().cpu(), o_out, atol=1.2e-2, rtol=6e-3)
+        torch.testing.assert_close(ref_imp.cpu(), o_imp, atol=3e-5, rtol=4e-4)
 
 
 def test_golden_fixtures():
