@@ -57,8 +57,8 @@ struct FusedPlan {
   const char* name;
 };
 
-// Fast path (fe_attn_fast.hip): D in {64, 128}, positive scale, 16-byte rows, buffer-
-// addressable K/V. Returns false (and leaves `plan` untouched) when it does not apply.
+// Fast path (fe_attn_fast.hip): D in {32, 64, 96, 128}, nonzero scale, 16-byte unit-stride
+// buffer-addressable K/V rows (Q of any strides). Returns false (and leaves `plan` untouched) when it does not apply.
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan);
 // Replay kernel of the split schedule (fe_attn_fast.hip): same layout rules as fast_plan;
 // launched with ReplayPlan::waves waves and ReplayPlan::rows row tiles per workgroup.

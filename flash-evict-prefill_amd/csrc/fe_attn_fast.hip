@@ -1,10 +1,11 @@
-// Fast path of the fused prefill kernel for gfx950: D in {64, 128}, positive softmax scale,
-// 16-byte K/V rows. Same mathematics as the generic kernel in fe_attn.hip (reference
+// Fast path of the fused prefill kernel for gfx950: D in {32, 64, 96, 128}, nonzero softmax
+// scale (a negative one runs as |scale| on -Q), 16-byte unit-stride K/V rows, Q of any strides. Same mathematics as the generic kernel in fe_attn.hip (reference
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
 //
 //   * A workgroup is NW waves of one 32-query row tile each, all on one KV head (GQA
 //     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. At
-//     D = 128 the kernels run 12 waves, three per SIMD; at D = 64, 8 (two workgroups per CU).
+//     D = 96 and 128 the kernels run 12 waves, three per SIMD; at D = 32 and 64, 8 (two
+//     workgroups per CU).
 //   * The K/V buffers hold pairs of 64-key tiles: one barrier per 128 keys.
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
@@ -723,10 +724,19 @@ ReplayPlan replay_entry(const char* name) {
   return ReplayPlan{(const void*)replay_fast_kernel<E, DP, FE_REPLAY_TPW>, 8 / FE_REPLAY_TPW, 8, name};
 }
 
+// Head dims of the fast kernels: multiples of 32 up to 128 (the tile DMA moves 32-channel
+// multiples, and two 2-tile buffers per operand must fit the LDS); the table index of D.
+constexpr int kFastDims = 4;
+int fast_slot(int D) { return (D == 32 || D == 64 || D == 96 || D == 128) ? D / 32 - 1 : -1; }
+
 ReplayPlan g_replay[] = {
+    replay_entry<F16, 32>("replay_fast<f16,32>"),
     replay_entry<F16, 64>("replay_fast<f16,64>"),
+    replay_entry<F16, 96>("replay_fast<f16,96>"),
     replay_entry<F16, 128>("replay_fast<f16,128>"),
+    replay_entry<BF16, 32>("replay_fast<bf16,32>"),
     replay_entry<BF16, 64>("replay_fast<bf16,64>"),
+    replay_entry<BF16, 96>("replay_fast<bf16,96>"),
     replay_entry<BF16, 128>("replay_fast<bf16,128>"),
 };
 
@@ -736,19 +746,30 @@ FusedPlan fast_entry(const char* name) {
 }
 
 // Per (dtype, D): the attention-only kernel (split schedule, or no importance) and the fused
-// kernel with the replay traversal (fe_prefill without a workspace). At D = 64 both stay at
-// 8 waves: about 115 registers and 68 KiB of LDS already put two workgroups, four waves per
-// SIMD, on a CU.
+// kernel with the replay traversal (fe_prefill without a workspace). At D = 32 and 64 both
+// stay at 8 waves: about 115 registers and 68 KiB of LDS at D = 64 already put two
+// workgroups, four waves per SIMD, on a CU. D = 96 runs 12 waves like D = 128 (96 KiB of
+// LDS: one workgroup per CU either way).
 FusedPlan g_fast[] = {
+    fast_entry<F16, 32, 8, false>("attn_fast<f16,32>"),
+    fast_entry<F16, 32, 8, true>("fused_fast<f16,32>"),
     fast_entry<F16, 64, 8, false>("attn_fast<f16,64>"),
     fast_entry<F16, 64, 8, true>("fused_fast<f16,64>"),
+    fast_entry<F16, 96, 12, false>("attn_fast<f16,96>"),
+    fast_entry<F16, 96, 12, true>("fused_fast<f16,96>"),
     fast_entry<F16, 128, 12, false>("attn_fast<f16,128>"),
     fast_entry<F16, 128, 12, true>("fused_fast<f16,128>"),
+    fast_entry<BF16, 32, 8, false>("attn_fast<bf16,32>"),
+    fast_entry<BF16, 32, 8, true>("fused_fast<bf16,32>"),
     fast_entry<BF16, 64, 8, false>("attn_fast<bf16,64>"),
     fast_entry<BF16, 64, 8, true>("fused_fast<bf16,64>"),
+    fast_entry<BF16, 96, 12, false>("attn_fast<bf16,96>"),
+    fast_entry<BF16, 96, 12, true>("fused_fast<bf16,96>"),
     fast_entry<BF16, 128, 12, false>("attn_fast<bf16,128>"),
     fast_entry<BF16, 128, 12, true>("fused_fast<bf16,128>"),
 };
+static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 2 * kFastDims, "replay table");
+static_assert(sizeof(g_fast) / sizeof(g_fast[0]) == 4 * kFastDims, "fast table");
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -761,14 +782,15 @@ bool kv_ok(const void* p, const long long* st, int N, int D) {
 }  // namespace
 
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
-  if (a.D != 64 && a.D != 128) return false;
+  const int slot = fast_slot(a.D);
+  if (slot < 0) return false;
   // Q is read once per row tile, element-wise when it is not 16-byte vectorisable (any
   // strides); K and V go through the tile DMA, which needs aligned unit-stride rows. A zero
   // scale takes the generic kernel.
   if (!(a.abs_scale_log2 > 0.f)) return false;
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
   const bool fused = a.score && !a.bias;
-  const int idx = 2 * ((dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0)) + (fused ? 1 : 0);
+  const int idx = 2 * ((dtype == 1 ? kFastDims : 0) + slot) + (fused ? 1 : 0);
   plan = g_fast[idx];
   return true;
 }
@@ -776,7 +798,7 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
 bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan) {
   FusedPlan fp;
   if (!fast_plan(a, dtype, fp)) return false;
-  plan = g_replay[(dtype == 1 ? 2 : 0) + (a.D == 128 ? 1 : 0)];
+  plan = g_replay[(dtype == 1 ? kFastDims : 0) + fast_slot(a.D)];
   return true;
 }
 

@@ -34,7 +34,7 @@ def cm_tile(dp, gb):
     return lds
 
 
-@pytest.mark.parametrize("dp", [64, 128])
+@pytest.mark.parametrize("dp", [32, 64, 96, 128])
 def test_cm_k_fragments(dp):
     lds = cm_tile(dp, 32)
     for s in range(2):
@@ -48,7 +48,7 @@ def test_cm_k_fragments(dp):
             assert all(len(set(b)) == 64 for b in phases.values())
 
 
-@pytest.mark.parametrize("dp", [64, 128])
+@pytest.mark.parametrize("dp", [32, 64, 96, 128])
 def test_cm_v_transposing_reads(dp):
     lds = cm_tile(dp, 64)
     for dt in range(dp // 32):
