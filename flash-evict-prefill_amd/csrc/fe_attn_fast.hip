@@ -1,5 +1,7 @@
-// Fast path of the fused prefill kernel for gfx950: D in {32, 64, 96, 128}, nonzero softmax
-// scale (a negative one runs as |scale| on -Q), 16-byte unit-stride K/V rows, Q of any strides. Same mathematics as the generic kernel in fe_attn.hip (reference
+// Fast path of the fused prefill kernel for gfx950: head dims that are a multiple of 8 up to
+// 128, on tile dims DP in {32, 64, 96, 128} (below DP the PARTIAL instantiation reads zeros
+// past channel D and stores D channels); nonzero softmax scale (a negative one runs as |scale|
+// on -Q), 16-byte unit-stride K/V rows, Q of any strides. Same mathematics as the generic kernel in fe_attn.hip (reference
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
 //
 //   * A workgroup is NW waves of one 32-query row tile each, all on one KV head (GQA
@@ -84,10 +86,13 @@ __device__ __forceinline__ float half_swap_maximum(float x) {
 // a 16-byte chunk of the group), so one offset register serves the whole tile. Rows past N
 // read as zero: a lane's offset reaches row N exactly when its row does, and 64r plus the
 // group width never exceeds the row (64(DPW - 1) + GB <= 2D), so an in-range row is read
-// whole.
-template <int DPW, int GB>
+// whole. PARTIAL (a head dim D below the tile's DP, D a multiple of 8): a lane whose 16-byte
+// chunk (channels g*GB/2 + dch .. +7 of block r's group g) starts at or past D takes an offset
+// past the record count, so it reads zeros and touches no memory; rows are never read past
+// their D channels, whatever the hardware does with the scalar offset.
+template <int DPW, int GB, bool PARTIAL = false>
 __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u32 doff, int kb, int N,
-                                            unsigned char* ldst, int wv) {
+                                            unsigned char* ldst, int wv, int D = 0, u32 dch = 0) {
   constexpr int KPB = 1024 / GB, BPG = 64 / KPB;
   static_assert(4 % BPG == 0 && (4 / BPG) * GB == 64, "one descriptor per wave");
   // recomputed per call: hoisting the per-block LDS addresses of every call site out of the
@@ -100,14 +105,20 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
       (void*)(g + (size_t)((u32)k0 * rowb) + (w / BPG) * GB), (short)0, nrec, 0x00020000);
   unsigned char* dst = ldst + w * 1024;
 #pragma unroll
-  for (int r = 0; r < DPW; ++r)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + r * 4096), 16, doff, 64 * r, 0, 0);
+  for (int r = 0; r < DPW; ++r) {
+    u32 off = doff;
+    if constexpr (PARTIAL) {
+      const u32 ch = (u32)((w / BPG + (4 / BPG) * r) * (GB / 2)) + dch;   // the lane's first channel
+      off = ch < (u32)D ? doff : 0x7fffffffu;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dst + r * 4096), 16, off, 64 * r, 0, 0);
+  }
 }
 
 // NW waves of one row tile each (8: two waves per SIMD; 12: three, at D = 128, which then
 // reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
-template <typename E, int DP, int NW, bool FUSED>
+template <typename E, int DP, int NW, bool FUSED, bool PARTIAL>
 __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, TILE = T::TILE;
@@ -161,7 +172,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
     const bool ok = tv && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
   }
 
   // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
@@ -189,8 +200,10 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
   const u32 dv = (u32)(lane >> 2) * vrow + (u32)((lane & 3) << 4);
   const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
   const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
-  auto dma_k = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 32>(kg, krow, dk, kb, N, ldst, wv); };
-  auto dma_v = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 64>(vg, vrow, dv, kb, N, ldst, wv); };
+  // PARTIAL: the lanes' first channel within their K (16-channel) and V (32-channel) group
+  const u32 dchk = (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 3), dchv = (u32)((lane & 3) << 3);
+  auto dma_k = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, dk, kb, N, ldst, wv, a.D, dchk); };
+  auto dma_v = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, dv, kb, N, ldst, wv, a.D, dchv); };
 
   // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunk pairs h*NDC/KH .. +NDC/KH
   auto k_frags = [&](int BUF, int SLOT, int s, int h, u32x4(&kf)[NDC / KH]) __attribute__((always_inline)) {
@@ -423,12 +436,13 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
     const int qi = q0 + l32;
     if (tv && qi < N) {
       const float inv = 1.f / half_swap_sum(l_rnd);
-      u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * DP;
+      u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * (PARTIAL ? a.D : DP);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+          if (PARTIAL && d0 >= a.D) continue;    // channels past D (a multiple of 8) are not stored
           const u32 w0 = E::pack2(o[dt][4 * g4 + 0] * inv, o[dt][4 * g4 + 1] * inv);
           const u32 w1 = E::pack2(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv);
           *(u32x2*)(op + d0) = (u32x2){w0, w1};
@@ -570,7 +584,7 @@ __device__ __forceinline__ int lane_now() {
   return l;
 }
 
-template <typename E, int DP, int TPW>
+template <typename E, int DP, int TPW, bool PARTIAL>
 __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, TILE = T::TILE;
@@ -627,7 +641,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
     const bool ok = rin && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     const float br = ok ? a.bias[(long long)(b * a.Hq + head) * N + qr] : POS_INF;
 #pragma unroll
     for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
@@ -638,6 +652,12 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
   const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
   const u32 krow = (u32)(a.ks[2] * 2);
   const u32 dk = (u32)(lane >> 1) * krow + (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
+  // PARTIAL: the lane's first channel in its K group, recomputed at each DMA (held across
+  // the loop it would be spilled at tile dim 128)
+  auto dchk = [&]() {
+    const int ln = lane_now();
+    return (u32)(((ln & 1) ^ ((ln >> 4) & 1)) << 3);
+  };
   const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
   float* imp_row = a.imp + (long long)bh * N;
 
@@ -658,7 +678,8 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
     if (dmaw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (it > it_lo) flush(kb - BN, BUF ^ 1);
-    if (dmaw && it + 1 < ntiles) dma_tile_cm<DPW, 32>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv);
+    if (dmaw && it + 1 < ntiles)
+      dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, dk, kb + BN, N, BUF == 0 ? lds_k1 : lds_k0, wv, a.D, PARTIAL ? dchk() : 0u);
     float cs[2] = {0.f, 0.f};
     if (kb <= wave_hi) {
       const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
@@ -705,7 +726,7 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
     }
   };
 
-  if (dmaw) dma_tile_cm<DPW, 32>(kg, krow, dk, it_lo * BN, N, lds_k0, wv);
+  if (dmaw) dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, dk, it_lo * BN, N, lds_k0, wv, a.D, PARTIAL ? dchk() : 0u);
   for (int it = it_lo; it < ntiles; it += 2) {
     step(it, 0);
     if (it + 1 < ntiles) step(it + 1, 1);
@@ -719,57 +740,48 @@ namespace {
 #ifndef FE_REPLAY_TPW
 #define FE_REPLAY_TPW 2
 #endif
-template <typename E, int DP>
+template <typename E, int DP, bool PARTIAL>
 ReplayPlan replay_entry(const char* name) {
-  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, FE_REPLAY_TPW>, 8 / FE_REPLAY_TPW, 8, name};
+  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, FE_REPLAY_TPW, PARTIAL>, 8 / FE_REPLAY_TPW, 8, name};
 }
 
-// Head dims of the fast kernels: multiples of 32 up to 128 (the tile DMA moves 32-channel
-// multiples, and two 2-tile buffers per operand must fit the LDS); the table index of D.
+// Tile dims of the fast kernels: multiples of 32 up to 128 (the tile DMA moves 32-channel
+// multiples, and two 2-tile buffers per operand must fit the LDS). A head dim D (a multiple of
+// 8, at most 128) runs on the tile dim DP = D rounded up to 32; when D < DP the PARTIAL
+// instantiation reads zeros past channel D and stores only D channels.
 constexpr int kFastDims = 4;
-int fast_slot(int D) { return (D == 32 || D == 64 || D == 96 || D == 128) ? D / 32 - 1 : -1; }
+int fast_slot(int D) { return (D >= 8 && D <= 128 && D % 8 == 0) ? (D + 31) / 32 - 1 : -1; }
 
-ReplayPlan g_replay[] = {
-    replay_entry<F16, 32>("replay_fast<f16,32>"),
-    replay_entry<F16, 64>("replay_fast<f16,64>"),
-    replay_entry<F16, 96>("replay_fast<f16,96>"),
-    replay_entry<F16, 128>("replay_fast<f16,128>"),
-    replay_entry<BF16, 32>("replay_fast<bf16,32>"),
-    replay_entry<BF16, 64>("replay_fast<bf16,64>"),
-    replay_entry<BF16, 96>("replay_fast<bf16,96>"),
-    replay_entry<BF16, 128>("replay_fast<bf16,128>"),
-};
+#define FE_REPLAY_ENTRIES(E, e)                                                                            \
+  replay_entry<E, 32, false>("replay_fast<" e ",32>"), replay_entry<E, 32, true>("replay_fast<" e ",32,partial>"), \
+      replay_entry<E, 64, false>("replay_fast<" e ",64>"), replay_entry<E, 64, true>("replay_fast<" e ",64,partial>"), \
+      replay_entry<E, 96, false>("replay_fast<" e ",96>"), replay_entry<E, 96, true>("replay_fast<" e ",96,partial>"), \
+      replay_entry<E, 128, false>("replay_fast<" e ",128>"), replay_entry<E, 128, true>("replay_fast<" e ",128,partial>")
+// [dtype][tile dim][partial]
+ReplayPlan g_replay[] = {FE_REPLAY_ENTRIES(F16, "f16"), FE_REPLAY_ENTRIES(BF16, "bf16")};
 
-template <typename E, int DP, int NW, bool FUSED>
+template <typename E, int DP, int NW, bool FUSED, bool PARTIAL>
 FusedPlan fast_entry(const char* name) {
-  return FusedPlan{(const void*)fused_fast_kernel<E, DP, NW, FUSED>, 0, NW, NW, name};   // static LDS only
+  return FusedPlan{(const void*)fused_fast_kernel<E, DP, NW, FUSED, PARTIAL>, 0, NW, NW, name};   // static LDS only
 }
 
-// Per (dtype, D): the attention-only kernel (split schedule, or no importance) and the fused
-// kernel with the replay traversal (fe_prefill without a workspace). At D = 32 and 64 both
-// stay at 8 waves: about 115 registers and 68 KiB of LDS at D = 64 already put two
-// workgroups, four waves per SIMD, on a CU. D = 96 runs 12 waves like D = 128 (96 KiB of
-// LDS: one workgroup per CU either way).
-FusedPlan g_fast[] = {
-    fast_entry<F16, 32, 8, false>("attn_fast<f16,32>"),
-    fast_entry<F16, 32, 8, true>("fused_fast<f16,32>"),
-    fast_entry<F16, 64, 8, false>("attn_fast<f16,64>"),
-    fast_entry<F16, 64, 8, true>("fused_fast<f16,64>"),
-    fast_entry<F16, 96, 12, false>("attn_fast<f16,96>"),
-    fast_entry<F16, 96, 12, true>("fused_fast<f16,96>"),
-    fast_entry<F16, 128, 12, false>("attn_fast<f16,128>"),
-    fast_entry<F16, 128, 12, true>("fused_fast<f16,128>"),
-    fast_entry<BF16, 32, 8, false>("attn_fast<bf16,32>"),
-    fast_entry<BF16, 32, 8, true>("fused_fast<bf16,32>"),
-    fast_entry<BF16, 64, 8, false>("attn_fast<bf16,64>"),
-    fast_entry<BF16, 64, 8, true>("fused_fast<bf16,64>"),
-    fast_entry<BF16, 96, 12, false>("attn_fast<bf16,96>"),
-    fast_entry<BF16, 96, 12, true>("fused_fast<bf16,96>"),
-    fast_entry<BF16, 128, 12, false>("attn_fast<bf16,128>"),
-    fast_entry<BF16, 128, 12, true>("fused_fast<bf16,128>"),
-};
-static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 2 * kFastDims, "replay table");
-static_assert(sizeof(g_fast) / sizeof(g_fast[0]) == 4 * kFastDims, "fast table");
+// Per (dtype, tile dim, partial): the attention-only kernel (split schedule, or no importance)
+// and the fused kernel with the replay traversal (fe_prefill without a workspace). At tile dims
+// 32 and 64 both stay at 8 waves: about 115 registers and 68 KiB of LDS at 64 already put two
+// workgroups, four waves per SIMD, on a CU. 96 runs 12 waves like 128 (96 KiB of LDS: one
+// workgroup per CU either way).
+#define FE_FAST_PAIR(E, e, DP, NW, P, ps)                                                      \
+  fast_entry<E, DP, NW, false, P>("attn_fast<" e "," #DP ps ">"),                               \
+      fast_entry<E, DP, NW, true, P>("fused_fast<" e "," #DP ps ">")
+#define FE_FAST_ENTRIES(E, e)                                                                                     \
+  FE_FAST_PAIR(E, e, 32, 8, false, ""), FE_FAST_PAIR(E, e, 32, 8, true, ",partial"),                              \
+      FE_FAST_PAIR(E, e, 64, 8, false, ""), FE_FAST_PAIR(E, e, 64, 8, true, ",partial"),                          \
+      FE_FAST_PAIR(E, e, 96, 12, false, ""), FE_FAST_PAIR(E, e, 96, 12, true, ",partial"),                        \
+      FE_FAST_PAIR(E, e, 128, 12, false, ""), FE_FAST_PAIR(E, e, 128, 12, true, ",partial")
+// [dtype][tile dim][partial][fused]
+FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")};
+static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 4 * kFastDims, "replay table");
+static_assert(sizeof(g_fast) / sizeof(g_fast[0]) == 8 * kFastDims, "fast table");
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -790,7 +802,8 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   if (!(a.abs_scale_log2 > 0.f)) return false;
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
   const bool fused = a.score && !a.bias;
-  const int idx = 2 * ((dtype == 1 ? kFastDims : 0) + slot) + (fused ? 1 : 0);
+  const int partial = a.D != 32 * (slot + 1) ? 1 : 0;
+  const int idx = 2 * (2 * ((dtype == 1 ? kFastDims : 0) + slot) + partial) + (fused ? 1 : 0);
   plan = g_fast[idx];
   return true;
 }
@@ -798,7 +811,8 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
 bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan) {
   FusedPlan fp;
   if (!fast_plan(a, dtype, fp)) return false;
-  plan = g_replay[(dtype == 1 ? kFastDims : 0) + fast_slot(a.D)];
+  const int slot = fast_slot(a.D);
+  plan = g_replay[2 * ((dtype == 1 ? kFastDims : 0) + slot) + (a.D != 32 * (slot + 1) ? 1 : 0)];
   return true;
 }
 

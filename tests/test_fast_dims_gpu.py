@@ -1,8 +1,10 @@
-"""Head dims 32 and 96 on the fast kernels (fe_attn_fast.hip instantiates D in {32, 64, 96,
-128}; other head dims take the generic kernel): the split schedule (prefill, with its
-workspace) and the fused single kernel (fe_prefill without a workspace) against the float64
-oracle, and against each other. The attention output of the two schedules is bitwise
-identical and their importance differs only by FP32 atomic order, as at D = 64 and 128."""
+"""Head dims other than 64 and 128 on the fast kernels (fe_attn_fast.hip: tile dims 32, 64,
+96 and 128; a head dim that is a multiple of 8 below its tile dim runs the PARTIAL
+instantiation, which reads zeros past channel D and stores D channels): the split schedule
+(prefill, with its workspace) and the fused single kernel (fe_prefill without a workspace)
+against the float64 oracle, and against each other. The attention output of the two
+schedules is bitwise identical and their importance differs only by FP32 atomic order, as
+at D = 64 and 128. Other head dims take the generic kernel."""
 import pytest
 import torch
 
@@ -23,7 +25,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("d", [32, 96])
+@pytest.mark.parametrize("d", [32, 96, 24, 80, 120])
 @pytest.mark.parametrize("n,hq,hk,dtype,causal,decay,window,layout", CASES)
 def test_fast_head_dims(d, n, hq, hk, dtype, causal, decay, window, layout):
     print(f"fast head dim d={d} n={n} hq={hq} hk={hk} {dtype} causal={causal} window={window}", flush=True)
@@ -43,12 +45,35 @@ def test_fast_head_dims(d, n, hq, hk, dtype, causal, decay, window, layout):
     assert float((imp - i2).abs().max()) <= 2e-6 * float(i2.abs().max())
 
 
+@pytest.mark.parametrize("d", [8, 40, 80, 120])
+def test_partial_head_dim_reads_stop_at_d(d):
+    # K and V rows of 2D channels whose channels past D are NaN: a read past channel D would
+    # put NaN into the logits (K) or, through the output store, into a neighbouring row
+    print(f"partial head dim d={d}: NaN past channel D", flush=True)
+    n, hq, hk = 333, 4, 2
+    q = seeded_randn((1, hq, n, d), torch.bfloat16, 70 + d)
+    wide_k = torch.full((1, hk, n, 2 * d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    wide_v = torch.full((1, hk, n, 2 * d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    wide_k[..., :d] = seeded_randn((1, hk, n, d), torch.bfloat16, 71 + d)
+    wide_v[..., :d] = seeded_randn((1, hk, n, d), torch.bfloat16, 72 + d)
+    k, v = wide_k[..., :d], wide_v[..., :d]
+    assert k.stride(2) == 2 * d and k.data_ptr() % 16 == 0
+    for use_ws in (True, False):
+        out, imp = _run(q, k, v, True, True, 0.0, 0, use_ws=use_ws)
+        assert torch.isfinite(out).all() and torch.isfinite(imp).all()
+        ref_out, ref_imp = chunked(q, k.contiguous(), v.contiguous(), block=512, dtype=torch.float64)
+        assert (out.double() - ref_out.to(out.device)).abs().max().item() <= 2e-2
+        assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+
+
 def test_fast_head_dim_kernels_listed():
     res = {r["kernel"]: r for r in flash_evict.kernel_resources()}
     for d in (32, 96):
-        for name in ("attn_fast<bf16,%d>" % d, "fused_fast<bf16,%d>" % d, "replay_fast<bf16,%d>" % d):
-            assert name in res
-            assert res[name]["scratch_bytes_per_thread"] == 0
+        for part in ("", ",partial"):
+            for name in ("attn_fast<bf16,%d%s>" % (d, part), "fused_fast<bf16,%d%s>" % (d, part),
+                         "replay_fast<bf16,%d%s>" % (d, part)):
+                assert name in res
+                assert res[name]["scratch_bytes_per_thread"] == 0
     # D = 96 runs twelve waves (three per SIMD), D = 32 eight
     assert res["attn_fast<bf16,96>"]["registers_per_thread"] <= 168
     assert res["attn_fast<bf16,96>"]["max_threads_per_block"] >= 768

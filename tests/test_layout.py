@@ -63,3 +63,34 @@ def test_cm_v_transposing_reads(dp):
                     assert [lds[a + x] for x in range(8)] == [(key, 2 * d + x) for x in range(8)]
                     phases.setdefault(lane // 32, []).extend((a // 4 + i) % 64 for i in range(2))
                 assert all(len(set(b)) == 64 for b in phases.values())
+
+
+@pytest.mark.parametrize("dp,d", [(32, 8), (32, 24), (64, 40), (64, 48), (96, 72), (96, 80), (128, 104), (128, 120)])
+@pytest.mark.parametrize("gb", [32, 64])
+def test_cm_partial_head_dim(dp, d, gb):
+    # dma_tile_cm<DPW, GB, PARTIAL>: a lane's first channel, (group of block r) * GB/2 + dch, is
+    # the channel its 16-byte read starts at; lanes at or past D read zeros (offset past the
+    # record count), and every lane that reads stays inside the row's D channels
+    rowb_dense = 2 * dp
+    dpw = (64 * (dp // 8)) // 256
+    kpb = 1024 // gb
+    bpg = 64 // kpb
+    zeros = set()
+    for wv in range(4):
+        for r in range(dpw):
+            for lane in range(64):
+                if gb == 32:
+                    doff = (lane >> 1) * rowb_dense + (((lane & 1) ^ ((lane >> 4) & 1)) << 4)
+                    dch = ((lane & 1) ^ ((lane >> 4) & 1)) << 3
+                else:
+                    doff = (lane >> 2) * rowb_dense + ((lane & 3) << 4)
+                    dch = (lane & 3) << 3
+                byte = (wv // bpg) * gb + 64 * r + doff % rowb_dense
+                ch = (wv // bpg + (4 // bpg) * r) * (gb // 2) + dch
+                assert ch == byte // 2
+                if ch < d:
+                    assert byte + 16 <= 2 * d
+                else:
+                    zeros.add((wv, r, lane))
+    # the zero lanes are exactly the chunks of channels d .. dp-1 of every key
+    assert len(zeros) * 8 == 64 * (dp - d)
