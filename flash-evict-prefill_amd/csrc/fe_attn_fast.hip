@@ -584,12 +584,23 @@ __device__ __forceinline__ int lane_now() {
   return l;
 }
 
+// Waves and row tiles of a replay workgroup: 8 row tiles as 8/TPW waves for TPW = 1 or 2;
+// TPW = 3 runs 4 waves of three row tiles (12 per workgroup, two waves per SIMD).
+template <int TPW>
+struct ReplayShape {
+  static constexpr int NW = TPW == 3 ? 4 : 8 / TPW;
+  static constexpr int RT = NW * TPW;
+  static constexpr int WAVES_PER_EU = TPW == 1 ? 4 : (TPW == 2 ? 3 : 2);
+};
+
 template <typename E, int DP, int TPW, bool PARTIAL>
-__global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * ReplayShape<TPW>::NW, ReplayShape<TPW>::WAVES_PER_EU) void replay_fast_kernel(
+    const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
-  constexpr int NW = 8 / TPW;                    // waves per workgroup
+  constexpr int NW = ReplayShape<TPW>::NW;       // waves per workgroup
+  constexpr int RT = ReplayShape<TPW>::RT;       // row tiles per workgroup
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -610,8 +621,8 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
   const int bh = rest % a.BH;
   const int wg = a.wg_bh - 1 - rest / a.BH;
   const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
-  const int t_begin = wg * 8;
-  const int t_end = min(a.tiles_bh, t_begin + 8);
+  const int t_begin = wg * RT;
+  const int t_end = min(a.tiles_bh, t_begin + RT);
   const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
   const int kv_end = a.causal ? wg_q_hi : N;
   const int ntiles_all = (kv_end + BN - 1) / BN;
@@ -737,12 +748,21 @@ __global__ __launch_bounds__(512 / TPW, TPW == 1 ? 4 : 3) void replay_fast_kerne
 
 namespace {
 
+// Row tiles per replay wave (build options; two by default). Three at tile dim 128 (252
+// registers, two waves per SIMD, each K fragment read from LDS feeding three MFMAs) replayed all
+// rows of the headline shape 1.3% faster but the headline's 1050 rows 0.5% slower (fewer,
+// larger workgroups); below 128 three were 3-13% slower.
 #ifndef FE_REPLAY_TPW
 #define FE_REPLAY_TPW 2
 #endif
+#ifndef FE_REPLAY_TPW128
+#define FE_REPLAY_TPW128 2
+#endif
 template <typename E, int DP, bool PARTIAL>
 ReplayPlan replay_entry(const char* name) {
-  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, FE_REPLAY_TPW, PARTIAL>, 8 / FE_REPLAY_TPW, 8, name};
+  constexpr int TPW = DP == 128 ? FE_REPLAY_TPW128 : FE_REPLAY_TPW;
+  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, TPW, PARTIAL>, ReplayShape<TPW>::NW, ReplayShape<TPW>::RT,
+                    name};
 }
 
 // Tile dims of the fast kernels: multiples of 32 up to 128 (the tile DMA moves 32-channel
