@@ -1,6 +1,6 @@
 """Seeded randomized parity sweep of the workspace-free entry point fe_prefill (the single
-fused attention + replay kernel: 12 waves at D = 128, 8 at D = 64; the generic kernel for
-other head dims) against the dense FP32 oracle (oracle/attention.materialized, restating
+fused attention + replay kernel: 12 waves on tile dims 96 and 128, 8 on 32 and 64; head dims
+below their tile dim on the partial instantiations) against the dense FP32 oracle (oracle/attention.materialized, restating
 reference.py:5-25), at the reference's tolerances (tests/test_prefill.py: bf16 .012/.006,
 fp16 .002/.006). Shapes, GQA groups, ragged N, dtypes, masks, windows, decays, scales and
 layouts are drawn from a seeded generator."""
@@ -21,7 +21,7 @@ def draw(seed):
     r = random.Random(5000 + seed)
     n = r.choice([1, 31, 64, 65, 127, 129, 300, 511, 700, 1025])
     return dict(b=r.choice([1, 1, 2]), hk=r.choice([1, 2, 4]), g=r.choice([1, 2, 4, 7]), n=n,
-                d=r.choice([64, 128, 128, 80]), dtype=r.choice([torch.float16, torch.bfloat16]),
+                d=r.choice([40, 64, 80, 96, 120, 128, 128]), dtype=r.choice([torch.float16, torch.bfloat16]),
                 causal=r.random() < 0.8, decay=r.choice([0.0, 0.0, 0.05, 0.5, 50.0]),
                 window=r.choice([0, 0, 1, 17, 64, n + 5]), weighted=r.random() < 0.7,
                 transposed=r.random() < 0.5)

@@ -1,8 +1,8 @@
 """Seeded randomized parity sweep of prefill/evict against the oracle.
 
 Each case draws its shape and options from a seeded generator: batch, KV heads and GQA group
-(1, 2, 4 or 7), N from 1 to 700 (tile edges included), head dims 16..256 (fast and generic
-kernels), fp16/bf16, causal or not, softmax scale (default, small, negative), recency decay
+(1, 2, 4 or 7), N from 1 to 700 (tile edges included), head dims 16..256 (the fast kernels for
+multiples of 8 up to 128, on full and partial tiles; the generic kernel above 128 and for 100), fp16/bf16, causal or not, softmax scale (default, small, negative), recency decay
 (including decays large enough that the replay keeps only a few rows), observation window,
 value weighting, contiguous or transposed layouts, and a selection budget, reserved suffix and
 pool kernel. The attention output and importance are compared with the dense FP32 oracle
@@ -29,7 +29,7 @@ def draw(seed):
     budget = r.randint(1, n)
     return dict(
         b=r.choice([1, 1, 2]), hk=r.choice([1, 2, 4]), g=r.choice([1, 2, 4, 7]), n=n,
-        d=r.choice([16, 32, 64, 64, 80, 128, 128, 160, 256]), dtype=r.choice([torch.float16, torch.bfloat16]),
+        d=r.choice([16, 32, 48, 64, 64, 80, 96, 100, 120, 128, 128, 160, 256]), dtype=r.choice([torch.float16, torch.bfloat16]),
         causal=r.random() < 0.8, scale=r.choice([None, None, 0.05, 0.3, -0.2]),
         decay=r.choice([0.0, 0.0, 0.05, 0.5, 3.0, 50.0]), window=r.choice([0, 0, 1, 17, 64, n + 5]),
         weighted=r.random() < 0.7, transposed=r.random() < 0.5, budget=budget,
