@@ -16,6 +16,7 @@ CASES = [
     (8, 32768, 1024, 64, 1, False), (8, 32768, 3277, 0, 1, False), (4, 32768, 2048, 64, 5, False),
     (5, 4000, 400, 0, 1, True), (2, 5000, 2500, 100, 3, True), (7, 2049, 2049, 0, 1, False),
     (6, 3000, 1000, 1000, 7, False), (1, 131072, 1024, 64, 1, False), (3, 70000, 17, 5, 9, True),
+    (2, 5000, 300, 10, 11, False), (2, 3000, 200, 0, 201, False), (2, 20000, 700, 3, 5, True),
 ]
 
 
