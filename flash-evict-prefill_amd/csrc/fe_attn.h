@@ -57,7 +57,7 @@ struct FusedPlan {
   const char* name;
 };
 
-// Fast path (fe_attn_fast.hip): D a multiple of 8 up to 128, nonzero scale, 16-byte unit-stride
+// Fast path (fe_attn_fast.hip): D a multiple of 8 up to 256, nonzero scale, 16-byte unit-stride
 // buffer-addressable K/V rows (Q of any strides). Returns false (and leaves `plan` untouched) when it does not apply.
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan);
 // Replay kernel of the split schedule (fe_attn_fast.hip): same layout rules as fast_plan;

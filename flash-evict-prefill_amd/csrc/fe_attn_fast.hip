@@ -1,5 +1,5 @@
 // Fast path of the fused prefill kernel for gfx950: head dims that are a multiple of 8 up to
-// 128, on tile dims DP in {32, 64, 96, 128} (below DP the PARTIAL instantiation reads zeros
+// 256, on tile dims DP in {32, 64, ..., 256} (below DP the PARTIAL instantiation reads zeros
 // past channel D and stores D channels); nonzero softmax scale (a negative one runs as |scale|
 // on -Q), 16-byte unit-stride K/V rows, Q of any strides. Same mathematics as the generic kernel in fe_attn.hip (reference
 // flash_evict/prefill.py:14-83); the differences are in data movement and instruction count:
@@ -7,8 +7,9 @@
 //   * A workgroup is NW waves of one 32-query row tile each, all on one KV head (GQA
 //     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. At
 //     D = 96 and 128 the kernels run 12 waves, three per SIMD; at D = 32 and 64, 8 (two
-//     workgroups per CU).
-//   * The K/V buffers hold pairs of 64-key tiles: one barrier per 128 keys.
+//     workgroups per CU); at 160 and 192, 8 (two per SIMD); at 224 and 256, 4 (one per SIMD).
+//   * The K/V buffers hold pairs of 64-key tiles up to tile dim 128 (one barrier per 128
+//     keys), single tiles above it (one barrier per 64 keys).
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
 //     staging registers; the tile's base and record count live in the buffer descriptor
 //     (scalar arithmetic only), so rows past N read as zero and no VALU work is spent on
@@ -118,12 +119,23 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
 // NW waves of one row tile each (8: two waves per SIMD; 12: three, at D = 128, which then
 // reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
+// Waves per SIMD the fused_fast_kernel instantiation is built for: 12-wave workgroups three,
+// 8-wave ones two, 4-wave ones (tile dim 256: 128 accumulator and 64 Q registers per wave) one.
+template <int NW>
+struct FastOccupancy {
+  static constexpr int WAVES_PER_EU = NW > 8 ? 3 : (NW > 4 ? 2 : 1);
+};
+
 template <typename E, int DP, int NW, bool FUSED, bool PARTIAL>
-__global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
-  constexpr int KH = NW > 8 ? 2 : 1;             // K fragment reads per 32-key half
+  constexpr int KH = (NW > 8 || DP > 128) ? 2 : 1;   // K fragment reads per 32-key half
+  // 64-key tiles per LDS buffer: two up to tile dim 128 (one barrier per pair of tiles), one
+  // above it, where two double-buffered pairs of K and V tiles would not fit the LDS
+  constexpr int SLOTS = DP <= 128 ? 2 : 1;
+  static_assert(NDC % KH == 0, "K fragment groups");
   static_assert(NW % 2 == 0 && NW >= 4, "row tiles per workgroup");
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
@@ -132,8 +144,8 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
   // one buffer) and the fragment reads of the other buffer do not alias, and the objects'
   // addresses are link-time constants that fold into the reads' offset fields.
   // Two buffers per operand, each holding two consecutive 64-key tiles (slots 0 and 1).
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[2 * TILE], lds_k1[2 * TILE], lds_v0[2 * TILE],
-      lds_v1[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[SLOTS * TILE], lds_k1[SLOTS * TILE],
+      lds_v0[SLOTS * TILE], lds_v1[SLOTS * TILE];
   __shared__ float red[FUSED ? 2 * NW * BN : 1];  // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
@@ -241,10 +253,10 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
     __syncthreads();
     if (dmaw) {
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl)
-        if (it + 2 + sl < ntiles) {
-          dma_k((it + 2 + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
-          dma_v((it + 2 + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+      for (int sl = 0; sl < SLOTS; ++sl)
+        if (it + SLOTS + sl < ntiles) {
+          dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+          dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
         }
     }
   };
@@ -405,7 +417,7 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
 
   if (dmaw) {
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
+    for (int sl = 0; sl < SLOTS; ++sl)
       if (sl < ntiles) {
         dma_k(sl * BN, lds_k0 + sl * TILE);
         dma_v(sl * BN, lds_v0 + sl * TILE);
@@ -414,14 +426,25 @@ __global__ __launch_bounds__(NW * 64, NW > 8 ? 3 : 2) void fused_fast_kernel(con
   // The tile loop is instantiated twice, with and without the FP32 sum of the replay rows,
   // and each wave runs one of them: the choice is made once per wave, not per tile.
   auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
-    for (int it = 0; it < ntiles; it += 4) {
-      t1_sync(it, 0);
-      t1_step(exact_tag, it, 0, 0);
-      if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
-      if (it + 2 < ntiles) {
-        t1_sync(it + 2, 1);
-        t1_step(exact_tag, it + 2, 1, 0);
-        if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+    if constexpr (SLOTS == 2) {
+      for (int it = 0; it < ntiles; it += 4) {
+        t1_sync(it, 0);
+        t1_step(exact_tag, it, 0, 0);
+        if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
+        if (it + 2 < ntiles) {
+          t1_sync(it + 2, 1);
+          t1_step(exact_tag, it + 2, 1, 0);
+          if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+        }
+      }
+    } else {
+      for (int it = 0; it < ntiles; it += 2) {
+        t1_sync(it, 0);
+        t1_step(exact_tag, it, 0, 0);
+        if (it + 1 < ntiles) {
+          t1_sync(it + 1, 1);
+          t1_step(exact_tag, it + 1, 1, 0);
+        }
       }
     }
   };
@@ -585,22 +608,24 @@ __device__ __forceinline__ int lane_now() {
 }
 
 // Waves and row tiles of a replay workgroup: 8 row tiles as 8/TPW waves for TPW = 1 or 2;
-// TPW = 3 runs 4 waves of three row tiles (12 per workgroup, two waves per SIMD).
-template <int TPW>
+// TPW = 3 runs 4 waves of three row tiles (12 per workgroup, two waves per SIMD). Above tile
+// dim 128 (one row tile per wave) the Q fragments alone take up to 64 registers: two waves per
+// SIMD.
+template <int TPW, int DP>
 struct ReplayShape {
   static constexpr int NW = TPW == 3 ? 4 : 8 / TPW;
   static constexpr int RT = NW * TPW;
-  static constexpr int WAVES_PER_EU = TPW == 1 ? 4 : (TPW == 2 ? 3 : 2);
+  static constexpr int WAVES_PER_EU = TPW == 1 ? (DP > 128 ? 2 : 4) : (TPW == 2 ? 3 : 2);
 };
 
 template <typename E, int DP, int TPW, bool PARTIAL>
-__global__ __launch_bounds__(64 * ReplayShape<TPW>::NW, ReplayShape<TPW>::WAVES_PER_EU) void replay_fast_kernel(
+__global__ __launch_bounds__((64 * ReplayShape<TPW, DP>::NW), (ReplayShape<TPW, DP>::WAVES_PER_EU)) void replay_fast_kernel(
     const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
-  constexpr int NW = ReplayShape<TPW>::NW;       // waves per workgroup
-  constexpr int RT = ReplayShape<TPW>::RT;       // row tiles per workgroup
+  constexpr int NW = ReplayShape<TPW, DP>::NW;   // waves per workgroup
+  constexpr int RT = ReplayShape<TPW, DP>::RT;   // row tiles per workgroup
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -760,23 +785,23 @@ namespace {
 #endif
 template <typename E, int DP, bool PARTIAL>
 ReplayPlan replay_entry(const char* name) {
-  constexpr int TPW = DP == 128 ? FE_REPLAY_TPW128 : FE_REPLAY_TPW;
-  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, TPW, PARTIAL>, ReplayShape<TPW>::NW, ReplayShape<TPW>::RT,
-                    name};
+  constexpr int TPW = DP > 128 ? 1 : (DP == 128 ? FE_REPLAY_TPW128 : FE_REPLAY_TPW);
+  return ReplayPlan{(const void*)replay_fast_kernel<E, DP, TPW, PARTIAL>, ReplayShape<TPW, DP>::NW,
+                    ReplayShape<TPW, DP>::RT, name};
 }
 
-// Tile dims of the fast kernels: multiples of 32 up to 128 (the tile DMA moves 32-channel
-// multiples, and two 2-tile buffers per operand must fit the LDS). A head dim D (a multiple of
-// 8, at most 128) runs on the tile dim DP = D rounded up to 32; when D < DP the PARTIAL
+// Tile dims of the fast kernels: multiples of 32 up to 256 (the tile DMA moves 32-channel
+// multiples; above 128 each LDS buffer holds one tile instead of two). A head dim D (a multiple
+// of 8, at most 256) runs on the tile dim DP = D rounded up to 32; when D < DP the PARTIAL
 // instantiation reads zeros past channel D and stores only D channels.
-constexpr int kFastDims = 4;
-int fast_slot(int D) { return (D >= 8 && D <= 128 && D % 8 == 0) ? (D + 31) / 32 - 1 : -1; }
+constexpr int kFastDims = 8;
+int fast_slot(int D) { return (D >= 8 && D <= 256 && D % 8 == 0) ? (D + 31) / 32 - 1 : -1; }
 
-#define FE_REPLAY_ENTRIES(E, e)                                                                            \
-  replay_entry<E, 32, false>("replay_fast<" e ",32>"), replay_entry<E, 32, true>("replay_fast<" e ",32,partial>"), \
-      replay_entry<E, 64, false>("replay_fast<" e ",64>"), replay_entry<E, 64, true>("replay_fast<" e ",64,partial>"), \
-      replay_entry<E, 96, false>("replay_fast<" e ",96>"), replay_entry<E, 96, true>("replay_fast<" e ",96,partial>"), \
-      replay_entry<E, 128, false>("replay_fast<" e ",128>"), replay_entry<E, 128, true>("replay_fast<" e ",128,partial>")
+#define FE_REPLAY_PAIR(E, e, DP) \
+  replay_entry<E, DP, false>("replay_fast<" e "," #DP ">"), replay_entry<E, DP, true>("replay_fast<" e "," #DP ",partial>")
+#define FE_REPLAY_ENTRIES(E, e)                                                                                   \
+  FE_REPLAY_PAIR(E, e, 32), FE_REPLAY_PAIR(E, e, 64), FE_REPLAY_PAIR(E, e, 96), FE_REPLAY_PAIR(E, e, 128),          \
+      FE_REPLAY_PAIR(E, e, 160), FE_REPLAY_PAIR(E, e, 192), FE_REPLAY_PAIR(E, e, 224), FE_REPLAY_PAIR(E, e, 256)
 // [dtype][tile dim][partial]
 ReplayPlan g_replay[] = {FE_REPLAY_ENTRIES(F16, "f16"), FE_REPLAY_ENTRIES(BF16, "bf16")};
 
@@ -793,11 +818,10 @@ FusedPlan fast_entry(const char* name) {
 #define FE_FAST_PAIR(E, e, DP, NW, P, ps)                                                      \
   fast_entry<E, DP, NW, false, P>("attn_fast<" e "," #DP ps ">"),                               \
       fast_entry<E, DP, NW, true, P>("fused_fast<" e "," #DP ps ">")
+#define FE_FAST_DIM(E, e, DP, NW) FE_FAST_PAIR(E, e, DP, NW, false, ""), FE_FAST_PAIR(E, e, DP, NW, true, ",partial")
 #define FE_FAST_ENTRIES(E, e)                                                                                     \
-  FE_FAST_PAIR(E, e, 32, 8, false, ""), FE_FAST_PAIR(E, e, 32, 8, true, ",partial"),                              \
-      FE_FAST_PAIR(E, e, 64, 8, false, ""), FE_FAST_PAIR(E, e, 64, 8, true, ",partial"),                          \
-      FE_FAST_PAIR(E, e, 96, 12, false, ""), FE_FAST_PAIR(E, e, 96, 12, true, ",partial"),                        \
-      FE_FAST_PAIR(E, e, 128, 12, false, ""), FE_FAST_PAIR(E, e, 128, 12, true, ",partial")
+  FE_FAST_DIM(E, e, 32, 8), FE_FAST_DIM(E, e, 64, 8), FE_FAST_DIM(E, e, 96, 12), FE_FAST_DIM(E, e, 128, 12),      \
+      FE_FAST_DIM(E, e, 160, 8), FE_FAST_DIM(E, e, 192, 8), FE_FAST_DIM(E, e, 224, 4), FE_FAST_DIM(E, e, 256, 4)
 // [dtype][tile dim][partial][fused]
 FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")};
 static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 4 * kFastDims, "replay table");

@@ -26,11 +26,11 @@ Modes (q [1,H,N,D], k/v [1,Hkv,N,D] bf16):
                only 1 MiB, where they are launch-latency bound): achieved GB/s of
                algorithmic bytes (each input byte read once, each output byte written once)
   --generic    prefill on the shapes and layouts the gfx950 fast path does not take (head
-               dims above 128 or not a multiple of 8, a zero scale, K/V rows off 16-byte
-               alignment), next to the fast path at D = 32, 64, 80, 96 and 128 (and at D = 128
-               with a negative scale and with a channel-strided q, which it reads element-wise):
-               attention only, and with every row replayed; TFLOP/s of the work the caller
-               asked for (at D = 80 the kernels compute on 96-channel tiles)
+               dims that are not a multiple of 8, a zero scale, K/V rows off 16-byte
+               alignment), next to the fast path at D = 32, 64, 80, 96, 128, 192 and 256 (and
+               at D = 128 with a negative scale and with a channel-strided q, which it reads
+               element-wise): attention only, and with every row replayed; TFLOP/s of the work
+               the caller asked for (at D = 80 the kernels compute on 96-channel tiles)
 
 Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
 --dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
@@ -401,8 +401,10 @@ def generic_rows(repeats, n=8192, hq=32, hk=8):
              ("fast D=96", "fast", 96, lambda: inputs(96), None),
              ("fast D=32", "fast", 32, lambda: inputs(32), None),
              ("fast D=80", "fast", 80, lambda: inputs(80), None),
+             ("fast D=192", "fast", 192, lambda: inputs(192), None),
+             ("fast D=256", "fast", 256, lambda: inputs(256), None),
              ("generic D=100", "generic", 100, lambda: inputs(100), None),
-             ("generic D=256", "generic", 256, lambda: inputs(256), None),
+             ("generic D=256 zero scale", "generic", 256, lambda: inputs(256), 0.0),
              ("fast D=128 negative scale", "fast", 128, lambda: inputs(128), -(128 ** -0.5)),
              ("generic D=128 zero scale", "generic", 128, lambda: inputs(128), 0.0),
              ("fast D=128 q channel stride 2", "fast", 128, lambda: strided_q(128), None),

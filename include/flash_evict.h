@@ -83,7 +83,7 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
 /*
  * fe_prefill with a caller-provided workspace (same contract and results up to FP32
  * atomic order). With at least fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
- * score != 0, else 0) and the fast layouts (D a multiple of 8 up to 128, nonzero scale, unit-stride
+ * score != 0, else 0) and the fast layouts (D a multiple of 8 up to 256, nonzero scale, unit-stride
  * 16-byte aligned K/V rows; Q of any strides),
  * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
  * per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace. With less

@@ -1,5 +1,5 @@
 """Head dims other than 64 and 128 on the fast kernels (fe_attn_fast.hip: tile dims 32, 64,
-96 and 128; a head dim that is a multiple of 8 below its tile dim runs the PARTIAL
+96, ..., 256; a head dim that is a multiple of 8 below its tile dim runs the PARTIAL
 instantiation, which reads zeros past channel D and stores D channels): the split schedule
 (prefill, with its workspace) and the fused single kernel (fe_prefill without a workspace)
 against the float64 oracle, and against each other. The attention output of the two
@@ -25,7 +25,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("d", [32, 96, 24, 80, 120])
+@pytest.mark.parametrize("d", [32, 96, 24, 80, 120, 160, 200, 256])
 @pytest.mark.parametrize("n,hq,hk,dtype,causal,decay,window,layout", CASES)
 def test_fast_head_dims(d, n, hq, hk, dtype, causal, decay, window, layout):
     print(f"fast head dim d={d} n={n} hq={hq} hk={hk} {dtype} causal={causal} window={window}", flush=True)
@@ -45,7 +45,7 @@ def test_fast_head_dims(d, n, hq, hk, dtype, causal, decay, window, layout):
     assert float((imp - i2).abs().max()) <= 2e-6 * float(i2.abs().max())
 
 
-@pytest.mark.parametrize("d", [8, 40, 80, 120])
+@pytest.mark.parametrize("d", [8, 40, 80, 120, 200, 248])
 def test_partial_head_dim_reads_stop_at_d(d):
     # K and V rows of 2D channels whose channels past D are NaN: a read past channel D would
     # put NaN into the logits (K) or, through the output store, into a neighbouring row
@@ -68,12 +68,13 @@ def test_partial_head_dim_reads_stop_at_d(d):
 
 def test_fast_head_dim_kernels_listed():
     res = {r["kernel"]: r for r in flash_evict.kernel_resources()}
-    for d in (32, 96):
+    for d in (32, 96, 160, 256):
         for part in ("", ",partial"):
             for name in ("attn_fast<bf16,%d%s>" % (d, part), "fused_fast<bf16,%d%s>" % (d, part),
                          "replay_fast<bf16,%d%s>" % (d, part)):
                 assert name in res
                 assert res[name]["scratch_bytes_per_thread"] == 0
-    # D = 96 runs twelve waves (three per SIMD), D = 32 eight
+    # D = 96 runs twelve waves (three per SIMD), D = 32 eight, D = 256 four (one per SIMD)
     assert res["attn_fast<bf16,96>"]["registers_per_thread"] <= 168
     assert res["attn_fast<bf16,96>"]["max_threads_per_block"] >= 768
+    assert res["attn_fast<bf16,256>"]["max_threads_per_block"] >= 256

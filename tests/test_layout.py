@@ -34,7 +34,7 @@ def cm_tile(dp, gb):
     return lds
 
 
-@pytest.mark.parametrize("dp", [32, 64, 96, 128])
+@pytest.mark.parametrize("dp", [32, 64, 96, 128, 160, 192, 224, 256])
 def test_cm_k_fragments(dp):
     lds = cm_tile(dp, 32)
     for s in range(2):
@@ -48,7 +48,7 @@ def test_cm_k_fragments(dp):
             assert all(len(set(b)) == 64 for b in phases.values())
 
 
-@pytest.mark.parametrize("dp", [32, 64, 96, 128])
+@pytest.mark.parametrize("dp", [32, 64, 96, 128, 160, 192, 224, 256])
 def test_cm_v_transposing_reads(dp):
     lds = cm_tile(dp, 64)
     for dt in range(dp // 32):
@@ -65,7 +65,8 @@ def test_cm_v_transposing_reads(dp):
                 assert all(len(set(b)) == 64 for b in phases.values())
 
 
-@pytest.mark.parametrize("dp,d", [(32, 8), (32, 24), (64, 40), (64, 48), (96, 72), (96, 80), (128, 104), (128, 120)])
+@pytest.mark.parametrize("dp,d", [(32, 8), (32, 24), (64, 40), (64, 48), (96, 72), (96, 80), (128, 104), (128, 120),
+                                  (160, 136), (192, 184), (224, 200), (256, 232), (256, 248)])
 @pytest.mark.parametrize("gb", [32, 64])
 def test_cm_partial_head_dim(dp, d, gb):
     # dma_tile_cm<DPW, GB, PARTIAL>: a lane's first channel, (group of block r) * GB/2 + dch, is

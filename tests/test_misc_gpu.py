@@ -55,10 +55,10 @@ def test_generic_head_dims(d):
     torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("scale", [-0.1, 0.0, 0.5, 3.0])
 def test_scales(scale, d):
-    # D = 64/128: a negative scale runs on the fast kernels (|scale| on -Q), zero on the generic one
+    # a negative scale runs on the fast kernels (|scale| on -Q), zero on the generic one
     q, k, v = _qkv(n=130, d=d, seed=11)
     for causal in (True, False):
         out, imp = prefill(q, k, v, scale=scale, causal=causal)
