@@ -586,6 +586,360 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
   }
 }
 
+// The lane's index, recomputed where it is used: opaque to the compiler, which would
+// otherwise keep values derived from it live across a tile loop and, at two or three
+// waves per SIMD, spill them (each reload then waits behind the next tile's DMA).
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// Traversal 1 with two row tiles per wave (attention only: the split schedule, or no
+// importance), tile dims up to 128. Eight waves, two per SIMD, each holding the Q fragments
+// and O accumulators of two row tiles, so every K and V^T fragment read from LDS feeds two
+// MFMAs: half the LDS read traffic per MFMA of fused_fast_kernel, whose fragment reads cost
+// more than its exponentials. A 64-key tile runs as two 32-key halves (QK^T, mask,
+// probabilities, P@V of keys 32s .. 32s+31), which keeps S and P of both row tiles within
+// the 256 registers of a wave at two waves per SIMD.
+//
+// Same mathematics as fused_fast_kernel. The reference max of a row is the exact max of its
+// first 32 keys (instead of 64); the overflow guard, the rescale and the normalisation by the
+// sum of the rounded probabilities are per row tile and per half. Each row tile also hands
+// its replay bias to replay_fast_kernel, as fused_fast_kernel does.
+//
+// K fragments are read FE_RT2_KG at a time: two (250 registers, nothing spilled) and four
+// (one value spilled outside the tile loop) measured the same.
+#ifndef FE_RT2_KG
+#define FE_RT2_KG 2
+#endif
+template <typename E, int DP, bool PARTIAL>
+__global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
+  typedef FastTile<DP> T;
+  constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, TILE = T::TILE;
+  constexpr int DPW = T::DMA_PER_WAVE;
+  constexpr int NW = 8, RT = 2;                  // waves per workgroup, row tiles per wave
+  constexpr int SLOTS = 2;                       // 64-key tiles per LDS buffer
+  constexpr int KG = NDC >= FE_RT2_KG ? FE_RT2_KG : NDC;   // K fragments per read group
+  static_assert(DP <= 128 && NDC % KG == 0, "tile dims up to 128");
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  constexpr float POS_INF = __builtin_huge_valf();
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[SLOTS * TILE], lds_k1[SLOTS * TILE],
+      lds_v0[SLOTS * TILE], lds_v1[SLOTS * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
+  const int N = a.N;
+
+  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
+  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
+  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
+  const int t_begin = wg * (NW * RT);
+  const int t_end = min(a.tiles_bh, t_begin + NW * RT);
+  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
+  const int kv_end = a.causal ? wg_q_hi : N;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  // This wave's row tiles j = 0, 1: 32 query positions from q0[j] of query head head[j].
+  // lo_lim: below it no key of either tile is masked; wave_hi: past it every key of both tiles
+  // is.
+  int q0[RT], head[RT];
+  bool tv[RT];
+  int lo_lim = N, wave_hi = -1;
+  bool in_win = false;
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int t = t_begin + RT * wv + j;
+    tv[j] = t < t_end;
+    const int tt = tv[j] ? t : t_begin;
+    q0[j] = (tt / a.G) * 32;
+    head[j] = hkv * a.G + (tt - (tt / a.G) * a.G);
+    lo_lim = min(lo_lim, !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1));
+    wave_hi = max(wave_hi, !tv[j] ? -1 : (a.causal ? min(q0[j] + 31, N - 1) : N - 1));
+    in_win = in_win || (tv[j] && q0[j] + 31 >= a.win_lo);
+  }
+
+  const u32 qneg = a.neg_scale ? 0x80008000u : 0u;   // a negative scale runs as |scale| on -Q
+  u32x4 qf[RT][NDC];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const int qr = q0[j] + l32;
+    const bool ok = tv[j] && qr < N;
+    const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+#pragma unroll
+    for (int c = 0; c < NDC; ++c)
+      qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+  }
+
+  // LDS operand offsets and tile DMA: the layout of fused_fast_kernel
+  const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+  u32 voff;
+  {
+    const int r = lane & 15, g = lane >> 4;
+    voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
+  }
+  const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
+  const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+  const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
+  // per-lane DMA offsets (see fused_fast_kernel), recomputed at each DMA: held across the
+  // tile loop they would take registers the two row tiles need
+  auto dma_k = [&](int kb, unsigned char* ldst) {
+    const int ln = lane_now();
+    const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
+    dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
+  };
+  auto dma_v = [&](int kb, unsigned char* ldst) {
+    const int ln = lane_now();
+    dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, (u32)(ln >> 2) * vrow + (u32)((ln & 3) << 4), kb, N, ldst, wv, a.D,
+                                  (u32)((ln & 3) << 3));
+  };
+
+  // K fragments c0 .. c0+KG-1 of keys 32s + l32 (buffer BUF, slot SLOT)
+  auto k_frags = [&](int BUF, int SLOT, int s, int c0, u32x4(&kf)[KG]) __attribute__((always_inline)) {
+    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
+#pragma unroll
+    for (int c = 0; c < KG; ++c) kf[c] = *(const u32x4*)(kt + (c0 + c) * 2048);
+  };
+  auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
+    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
+    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
+    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+    return (u32x4){ux[0], ux[1], uy[0], uy[1]};
+  };
+
+  f32x16 o[RT][NDT];
+  // nm: minus the row's reference max (log2 units); 0 while a padding tile has seen no key
+  float l_run[RT], l_rnd[RT], nm[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    l_run[j] = 0.f;
+    l_rnd[j] = 0.f;
+    nm[j] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = (f32x16){};
+  }
+  bool fresh = true;                             // no key of this wave's tiles seen yet
+  // Only rows the replay visits need the FP32 sum (their replay bias); wave-uniform.
+  const bool exact_l = a.score && in_win;
+  u32 ones2;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
+
+  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (dmaw) {
+#pragma unroll
+      for (int sl = 0; sl < SLOTS; ++sl)
+        if (it + SLOTS + sl < ntiles) {
+          dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+          dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+        }
+    }
+  };
+  // Key kh + 8(i/4) + 4h + i%4 (accumulator register i) is visible to the lane's query row of
+  // tile j iff 8(i/4) + i%4 <= mask_rel(j, kh): the row's last visible key (-1 for a padding
+  // tile) minus kh + 4h. Lane-derived, so recomputed here (diagonal and ragged halves only).
+  auto mask_rel = [&](int j, int kh) __attribute__((always_inline)) -> int {
+    const int ln = lane_now();
+    const int ql = !tv[j] ? -1 : (a.causal ? min(q0[j] + (ln & 31), N - 1) : N - 1);
+    return ql - kh - 4 * (ln >> 5);
+  };
+  // S^T of keys kh .. kh+31 for both row tiles (lanes hold queries; register i holds key
+  // kh + 8(i/4) + 4h + i%4), masked on diagonal and ragged halves
+  auto qk_half = [&](int kh, int BUF, int SLOT, int s, f32x16(&S)[RT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < NDC / KG; ++g) {
+      u32x4 kf[KG];
+      k_frags(BUF, SLOT, s, g * KG, kf);
+      FE_PRIO_HI();
+#pragma unroll
+      for (int c = 0; c < KG; ++c)
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+          S[j] = (g == 0 && c == 0) ? E::mfma(kf[0], qf[j][0], (f32x16){}) : E::mfma(kf[c], qf[j][g * KG + c], S[j]);
+      FE_PRIO_LO();
+    }
+    if (kh + 31 > lo_lim) {
+#pragma unroll
+      for (int j = 0; j < RT; ++j) {
+        const int rel = mask_rel(j, kh);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[j][i] = 8 * (i >> 2) + (i & 3) <= rel ? S[j][i] : NEG_INF;
+      }
+    }
+  };
+  // the same for row tile J alone (the rare overflow recompute)
+  auto qk_one = [&](auto jtag, int kh, int BUF, int SLOT, int s, f32x16& S) __attribute__((always_inline)) {
+    constexpr int J = decltype(jtag)::value;
+#pragma unroll
+    for (int g = 0; g < NDC / KG; ++g) {
+      u32x4 kf[KG];
+      k_frags(BUF, SLOT, s, g * KG, kf);
+#pragma unroll
+      for (int c = 0; c < KG; ++c) S = (g == 0 && c == 0) ? E::mfma(kf[0], qf[J][0], (f32x16){}) : E::mfma(kf[c], qf[J][g * KG + c], S);
+    }
+    if (kh + 31 > lo_lim) {
+      const int rel = mask_rel(J, kh);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S[i] = 8 * (i >> 2) + (i & 3) <= rel ? S[i] : NEG_INF;
+    }
+  };
+  // exact max (log2 units) of a row over the 32 keys of S: this lane's 16 and the other half-wave's
+  auto exact_max = [&](const f32x16& S) __attribute__((always_inline)) -> float {
+    float mc = vmax(vmax(S[0], S[1]), S[2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2) mc = vmax(vmax(mc, S[i]), S[i + 1]);
+    return half_swap_maximum(vmax(mc, S[15])) * a.abs_scale_log2;
+  };
+  // P = exp2(S*scale - m) packed to the input dtype (pb[0]: keys 0-15 of the half, pb[1]:
+  // 16-31), partial sums of the rounded probabilities (pr); EXACT also returns the lane's
+  // FP32 sum of the unrounded ones
+  // S is consumed in place (it holds the probabilities afterwards).
+  auto probs = [&](auto exact_tag, f32x16& S, float nmj, u32x4(&pb)[2], float(&pr)[4]) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+    float ps[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      S[i] = fast_exp2(fmaf(S[i], a.abs_scale_log2, nmj));
+      if constexpr (EXACT) ps[i & 3] = i < 4 ? S[i] : ps[i & 3] + S[i];
+    }
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+      pb[c2] = (u32x4){E::pack2(S[8 * c2 + 0], S[8 * c2 + 1]), E::pack2(S[8 * c2 + 2], S[8 * c2 + 3]),
+                       E::pack2(S[8 * c2 + 4], S[8 * c2 + 5]), E::pack2(S[8 * c2 + 6], S[8 * c2 + 7])};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pr[e] = E::sum2(pb[1][e], ones2, E::sum2(pb[0][e], ones2, 0.f));
+    if constexpr (EXACT)
+      return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    else
+      return 0.f;
+  };
+  // overflow path of row tile J: S again, the new exact max, O and both sums rescaled,
+  // probabilities recomputed (now at most 1)
+  auto rescale_one = [&](auto exact_tag, auto jtag, int kh, int BUF, int SLOT, int s, u32x4(&pb)[2], float(&pr)[4])
+                         __attribute__((always_inline)) -> float {
+    constexpr int J = decltype(jtag)::value;
+    f32x16 S;
+    qk_one(jtag, kh, BUF, SLOT, s, S);
+    // a row that overflows has a finite reference max (its tile is a real one)
+    const float m_old = -nm[J];
+    const float mn = vmax(m_old, exact_max(S));
+    const float corr = mn > m_old ? fast_exp2(m_old - mn) : 1.f;
+    l_run[J] *= corr;
+    l_rnd[J] *= corr;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[J][dt] *= corr;
+    nm[J] = -mn;
+    return probs(exact_tag, S, nm[J], pb, pr);
+  };
+  // keys 32s .. 32s+31 of tile it (buffer BUF, slot SLOT)
+  auto t1_half = [&](auto exact_tag, int it, int BUF, int SLOT, int s) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+    const int kh = it * BN + 32 * s;
+    if (kh > wave_hi) return;
+
+    f32x16 S[RT];
+    qk_half(kh, BUF, SLOT, s, S);
+    if (fresh) {
+      // first keys of the row tiles (O and the sums are still zero): exact max, no rescale
+#pragma unroll
+      for (int j = 0; j < RT; ++j) {
+        const float mt = exact_max(S[j]);
+        nm[j] = mt == NEG_INF ? 0.f : -mt;
+      }
+      fresh = false;
+    }
+    u32x4 pb[RT][2];
+    float pr[RT][4], le[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) le[j] = probs(exact_tag, S[j], nm[j], pb[j], pr[j]);
+    {
+      const float g0 = EXACT ? le[0] : (pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3]);
+      if (__any(g0 > E::kMaxTileSum)) le[0] = rescale_one(exact_tag, std::integral_constant<int, 0>{}, kh, BUF, SLOT, s, pb[0], pr[0]);
+      const float g1 = EXACT ? le[1] : (pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]);
+      if (__any(g1 > E::kMaxTileSum)) le[1] = rescale_one(exact_tag, std::integral_constant<int, 1>{}, kh, BUF, SLOT, s, pb[1], pr[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      l_rnd[j] += (pr[j][0] + pr[j][1]) + (pr[j][2] + pr[j][3]);
+      if constexpr (EXACT) l_run[j] += le[j];
+    }
+    // O^T += V^T P^T over the half's two 16-key groups; each V^T fragment feeds both row tiles
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      u32x4 vf[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) vf[c] = v_frag(BUF, SLOT, 2 * s + c, dt);
+      FE_PRIO_HI();
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < RT; ++j) o[j][dt] = E::mfma(vf[c], pb[j][c], o[j][dt]);
+      FE_PRIO_LO();
+    }
+  };
+  auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
+    t1_half(exact_tag, it, BUF, SLOT, 0);
+    t1_half(exact_tag, it, BUF, SLOT, 1);
+  };
+
+  if (dmaw) {
+#pragma unroll
+    for (int sl = 0; sl < SLOTS; ++sl)
+      if (sl < ntiles) {
+        dma_k(sl * BN, lds_k0 + sl * TILE);
+        dma_v(sl * BN, lds_v0 + sl * TILE);
+      }
+  }
+  auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
+    for (int it = 0; it < ntiles; it += 4) {
+      t1_sync(it, 0);
+      t1_step(exact_tag, it, 0, 0);
+      if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
+      if (it + 2 < ntiles) {
+        t1_sync(it + 2, 1);
+        t1_step(exact_tag, it + 2, 1, 0);
+        if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+      }
+    }
+  };
+  if (exact_l)
+    t1_loop(std::true_type{});
+  else
+    t1_loop(std::false_type{});
+
+  // ---------------- finish rows: O / l_rnd, and the replay bias
+#pragma unroll
+  for (int j = 0; j < RT; ++j) {
+    const float l_tot = half_swap_sum(l_run[j]);
+    const float inv = 1.f / half_swap_sum(l_rnd[j]);
+    const int qi = q0[j] + l32;
+    if (tv[j] && qi < N) {
+      u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * (PARTIAL ? a.D : DP);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+          if (PARTIAL && d0 >= a.D) continue;
+          const u32 w0 = E::pack2(o[j][dt][4 * g4 + 0] * inv, o[j][dt][4 * g4 + 1] * inv);
+          const u32 w1 = E::pack2(o[j][dt][4 * g4 + 2] * inv, o[j][dt][4 * g4 + 3] * inv);
+          *(u32x2*)(op + d0) = (u32x2){w0, w1};
+        }
+      }
+      if (a.score && a.bias && hh == 0) {
+        const bool live = qi >= a.win_lo;
+        a.bias[(long long)(b * a.Hq + head[j]) * N + qi] =
+            live ? (fast_log2(l_tot) - nm[j] - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+      }
+    }
+  }
+}
+
 // Replay traversal of the split schedule. After fused_fast_kernel has written the bias
 //   b_q = m_q + log2 l_q - decay*log2e*(q - N + 1)   (+inf outside the window or past N)
 // of every query row, the importance is
@@ -598,14 +952,6 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
 // with every K fragment read from LDS feeding two MFMAs: that halves the LDS read
 // traffic, the co-bottleneck of this traversal next to the MFMAs, and measures about 3%
 // faster than TPW = 1. The K tiles use the attention kernel's channel-group-major layout.
-// The lane's index, recomputed where it is used: opaque to the compiler, which would
-// otherwise keep values derived from it live across the replay's tile loop and, at three
-// waves per SIMD, spill them (each reload then waits behind the next tile's DMA).
-__device__ __forceinline__ int lane_now() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
 
 // Waves and row tiles of a replay workgroup: 8 row tiles as 8/TPW waves for TPW = 1 or 2;
 // TPW = 3 runs 4 waves of three row tiles (12 per workgroup, two waves per SIMD). Above tile
@@ -824,6 +1170,14 @@ FusedPlan fast_entry(const char* name) {
       FE_FAST_DIM(E, e, 160, 8), FE_FAST_DIM(E, e, 192, 8), FE_FAST_DIM(E, e, 224, 4), FE_FAST_DIM(E, e, 256, 4)
 // [dtype][tile dim][partial][fused]
 FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")};
+// Attention-only traversal with two row tiles per wave at tile dim 128 (attn_rt2_kernel: 8
+// waves, 16 row tiles per workgroup), 3-5% faster than fused_fast_kernel's 12 waves of one
+// row tile on every measured configuration; -D FE_ATTN_RT2=0 restores the latter. [dtype]
+#ifndef FE_ATTN_RT2
+#define FE_ATTN_RT2 1
+#endif
+FusedPlan g_rt2[] = {FusedPlan{(const void*)attn_rt2_kernel<F16, 128, false>, 0, 8, 16, "attn_rt2<f16,128>"},
+                     FusedPlan{(const void*)attn_rt2_kernel<BF16, 128, false>, 0, 8, 16, "attn_rt2<bf16,128>"}};
 static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 4 * kFastDims, "replay table");
 static_assert(sizeof(g_fast) / sizeof(g_fast[0]) == 8 * kFastDims, "fast table");
 
@@ -847,6 +1201,10 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
   const bool fused = a.score && !a.bias;
   const int partial = a.D != 32 * (slot + 1) ? 1 : 0;
+  if (!fused && slot == 3 && !partial && FE_ATTN_RT2) {
+    plan = g_rt2[dtype == 1 ? 1 : 0];
+    return true;
+  }
   const int idx = 2 * (2 * ((dtype == 1 ? kFastDims : 0) + slot) + partial) + (fused ? 1 : 0);
   plan = g_fast[idx];
   return true;
@@ -872,9 +1230,9 @@ void append_fast_resources(std::string& out) {
              attr.maxThreadsPerBlock);
     out += buf;
   }
-  for (const auto& e : g_fast) {
+  auto plan_row = [&](const FusedPlan& e) {
     hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, e.fn) != hipSuccess) continue;
+    if (hipFuncGetAttributes(&attr, e.fn) != hipSuccess) return;
     char buf[512];
     snprintf(buf, sizeof(buf),
              "{\"kernel\":\"%s\",\"registers_per_thread\":%d,\"lds_static_bytes\":%zu,"
@@ -882,7 +1240,9 @@ void append_fast_resources(std::string& out) {
              e.name, attr.numRegs, (size_t)attr.sharedSizeBytes, e.lds, (size_t)attr.localSizeBytes,
              attr.maxThreadsPerBlock);
     out += buf;
-  }
+  };
+  for (const auto& e : g_fast) plan_row(e);
+  for (const auto& e : g_rt2) plan_row(e);
 }
 
 }  // namespace fe
