@@ -596,7 +596,7 @@ __device__ __forceinline__ int lane_now() {
 }
 
 // Traversal 1 with two row tiles per wave (attention only: the split schedule, or no
-// importance), tile dims up to 128. Eight waves, two per SIMD, each holding the Q fragments
+// importance), tile dims 96 and 128. Eight waves, two per SIMD, each holding the Q fragments
 // and O accumulators of two row tiles, so every K and V^T fragment read from LDS feeds two
 // MFMAs: half the LDS read traffic per MFMA of fused_fast_kernel, whose fragment reads cost
 // more than its exponentials. A 64-key tile runs as two 32-key halves (QK^T, mask,
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
   constexpr int NW = 8, RT = 2;                  // waves per workgroup, row tiles per wave
   constexpr int SLOTS = 2;                       // 64-key tiles per LDS buffer
   constexpr int KG = NDC >= FE_RT2_KG ? FE_RT2_KG : NDC;   // K fragments per read group
-  static_assert(DP <= 128 && NDC % KG == 0, "tile dims up to 128");
+  static_assert(DP >= 96 && DP <= 128 && NDC % KG == 0, "tile dims 96 and 128");
   constexpr float NEG_INF = -__builtin_huge_valf();
   constexpr float POS_INF = __builtin_huge_valf();
 
@@ -1170,14 +1170,24 @@ FusedPlan fast_entry(const char* name) {
       FE_FAST_DIM(E, e, 160, 8), FE_FAST_DIM(E, e, 192, 8), FE_FAST_DIM(E, e, 224, 4), FE_FAST_DIM(E, e, 256, 4)
 // [dtype][tile dim][partial][fused]
 FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")};
-// Attention-only traversal with two row tiles per wave at tile dim 128 (attn_rt2_kernel: 8
-// waves, 16 row tiles per workgroup), 3-5% faster than fused_fast_kernel's 12 waves of one
-// row tile on every measured configuration; -D FE_ATTN_RT2=0 restores the latter. [dtype]
+// Attention-only traversal with two row tiles per wave at tile dims 96 and 128 (attn_rt2_kernel:
+// 8 waves, 16 row tiles per workgroup), head dims below the tile dim included: 3-5% faster than
+// fused_fast_kernel's 12 waves of one row tile on every measured configuration at D = 128, 3% at
+// D = 80 and 96, 6% at D = 120 (B1 Hq32/Hkv8 N16384). At tile dim 64 (12 waves of two row tiles,
+// 152 registers, three per SIMD) it was 16% slower than the 8-wave kernel that runs two
+// workgroups per CU there, so 64 keeps that kernel. -D FE_ATTN_RT2=0 restores the 12-wave kernel
+// everywhere. Bit s of FE_ATTN_RT2 selects tile dim 32(s+1) (s = 2, 3).
 #ifndef FE_ATTN_RT2
-#define FE_ATTN_RT2 1
+#define FE_ATTN_RT2 12
 #endif
-FusedPlan g_rt2[] = {FusedPlan{(const void*)attn_rt2_kernel<F16, 128, false>, 0, 8, 16, "attn_rt2<f16,128>"},
-                     FusedPlan{(const void*)attn_rt2_kernel<BF16, 128, false>, 0, 8, 16, "attn_rt2<bf16,128>"}};
+#ifndef FE_ATTN_RT2_PARTIAL
+#define FE_ATTN_RT2_PARTIAL 1
+#endif
+#define FE_RT2_ENTRY(E, e, DP, P, ps) FusedPlan{(const void*)attn_rt2_kernel<E, DP, P>, 0, 8, 16, "attn_rt2<" e "," #DP ps ">"}
+#define FE_RT2_DIM(E, e, DP) FE_RT2_ENTRY(E, e, DP, false, ""), FE_RT2_ENTRY(E, e, DP, true, ",partial")
+#define FE_RT2_ENTRIES(E, e) FE_RT2_DIM(E, e, 96), FE_RT2_DIM(E, e, 128)
+// [dtype][tile dim 96, 128][partial]
+FusedPlan g_rt2[] = {FE_RT2_ENTRIES(F16, "f16"), FE_RT2_ENTRIES(BF16, "bf16")};
 static_assert(sizeof(g_replay) / sizeof(g_replay[0]) == 4 * kFastDims, "replay table");
 static_assert(sizeof(g_fast) / sizeof(g_fast[0]) == 8 * kFastDims, "fast table");
 
@@ -1201,8 +1211,8 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
   const bool fused = a.score && !a.bias;
   const int partial = a.D != 32 * (slot + 1) ? 1 : 0;
-  if (!fused && slot == 3 && !partial && FE_ATTN_RT2) {
-    plan = g_rt2[dtype == 1 ? 1 : 0];
+  if (!fused && (slot == 2 || slot == 3) && ((FE_ATTN_RT2 >> slot) & 1) && (!partial || FE_ATTN_RT2_PARTIAL)) {
+    plan = g_rt2[2 * (2 * (dtype == 1 ? 1 : 0) + slot - 2) + partial];
     return true;
   }
   const int idx = 2 * (2 * ((dtype == 1 ? kFastDims : 0) + slot) + partial) + (fused ? 1 : 0);

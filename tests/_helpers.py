@@ -67,6 +67,38 @@ def assert_importance_close(imp, ref, rtol=1e-3, floor=1e-30):
     return worst
 
 
+def split_runs_two_row_tiles(d):
+    """Whether the split schedule (fe_prefill_ws) runs the two-row-tile attention kernel at head
+    dim d in the default build: tile dims 96 and 128 (d a multiple of 8 in 72..128). Where it
+    does, its reference max comes from a row's first 32 keys, the fused kernel's from 64."""
+    return d % 8 == 0 and 72 <= d <= 128
+
+
+def assert_schedules_agree(o_split, o_fused, i_split, i_fused, v, hq, hk):
+    """Outputs and importance of the split and fused schedules on the same inputs.
+
+    Same attention kernel (bitwise-equal outputs): the importance differs only by the order of
+    FP32 atomic additions. Different attention kernels: the probabilities P = exp2(s*scale - m)
+    are rounded to the input dtype at other reference maxima m, so with rounding errors e1_k,
+    e2_k (|e| <= u: 2^-9 for bf16, 2^-12 for fp16) and d_k = e1_k - e2_k the outputs differ to
+    first order by sum_k w_k d_k (v_k - o), at most 2u (max_k |v_k| + |o|), plus one rounding
+    of each stored output: |o_split - o_fused| <= 2u max|v| + 4u |o| per query head. The replay
+    bias m + log2 l is then the same quantity summed in another order, so the importance agrees
+    to FP32 summation error (1e-4 element-wise, plus the atomic-order floor)."""
+    floor = 3e-6 * float(i_fused.abs().max())
+    if torch.equal(o_split, o_fused):
+        assert float((i_split - i_fused).abs().max()) <= floor
+        return
+    u = 2.0 ** -9 if o_split.dtype == torch.bfloat16 else 2.0 ** -12
+    vmax = v.float().abs().amax(dim=(2, 3)).repeat_interleave(hq // hk, dim=1)[:, :, None, None]
+    diff = (o_split.float() - o_fused.float()).abs()
+    bound = 2 * u * vmax + 4 * u * o_fused.float().abs()
+    print("schedules: max |o_split - o_fused| = %.3e, max rel importance diff = %.3e"
+          % (diff.max().item(), ((i_split - i_fused).abs() / (i_fused.abs() + 1e-30)).max().item()), flush=True)
+    assert bool((diff <= bound).all()), float((diff - bound).max())
+    assert bool(((i_split - i_fused).abs() <= 1e-4 * i_fused.abs() + floor).all())
+
+
 def out_err_all_rows(out, q, k, v, block=2048, **kw):
     """Max-abs error of the attention output against the FP32 oracle over every row of every
     query head, computed one head at a time (oracle.attention.chunked on out's device)."""

@@ -2,16 +2,19 @@
 96, ..., 256; a head dim that is a multiple of 8 below its tile dim runs the PARTIAL
 instantiation, which reads zeros past channel D and stores D channels): the split schedule
 (prefill, with its workspace) and the fused single kernel (fe_prefill without a workspace)
-against the float64 oracle, and against each other. The attention output of the two
-schedules is bitwise identical and their importance differs only by FP32 atomic order, as
-at D = 64 and 128. Other head dims take the generic kernel."""
+against the float64 oracle, and against each other: where both schedules run the same
+attention kernel their outputs are bitwise identical and their importance differs only by
+FP32 atomic order; at tile dims 96 and 128 the split schedule runs the two-row-tile kernel and
+the schedules agree within the derived rounding bound (assert_schedules_agree). Other head
+dims take the generic kernel."""
 import pytest
 import torch
 
 import flash_evict
 from flash_evict import prefill
 from oracle.attention import chunked
-from _helpers import assert_importance_close, seeded_randn, transposed_qkv
+from _helpers import (assert_importance_close, assert_schedules_agree, seeded_randn, split_runs_two_row_tiles,
+                      transposed_qkv)
 from test_schedules_gpu import _run
 
 pytestmark = pytest.mark.gpu
@@ -41,8 +44,9 @@ def test_fast_head_dims(d, n, hq, hk, dtype, causal, decay, window, layout):
     assert (out.double() - ref_out.to(out.device)).abs().max().item() <= (2e-2 if dtype == torch.bfloat16 else 5e-3)
     assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
     o2, i2 = _run(q, k, v, causal, True, decay, window, use_ws=False)
-    assert torch.equal(out, o2)
-    assert float((imp - i2).abs().max()) <= 2e-6 * float(i2.abs().max())
+    if not split_runs_two_row_tiles(d):
+        assert torch.equal(out, o2)
+    assert_schedules_agree(out, o2, imp, i2, v, hq, hk)
 
 
 @pytest.mark.parametrize("d", [8, 40, 80, 120, 200, 248])
