@@ -463,31 +463,35 @@ __device__ __forceinline__ void write_suffix(int m, int K, int recent, long long
 }
 
 // out[r, i] = (sum_{j=i-k/2}^{i+k/2} past[r, j], zeros outside [0, m)) / k, summed left to
-// right (the order of torch's avg_pool kernels). Each 256-thread block stages its kPoolTile
+// right (the order of torch's avg_pool kernels). Each 256-thread block stages its `tile`
 // outputs' inputs (plus the k/2 halo on each side) in LDS once; the window sum is unrolled
-// for the usual small k (KT > 0), a loop otherwise. (A float4 variant of the full tiles, with
-// 16-byte loads, LDS reads and stores, measured no faster: the kernel moves about 4 TB/s of
-// reads and writes either way.)
+// for the usual small k (KT > 0), a loop otherwise. The host picks the tile: kPoolTile
+// outputs per block on large inputs, halved down to 256 until the grid has enough blocks to
+// fill the chip (8 rows x 32K scores: 64 blocks of 4096 outputs took 9 us). (A float4 variant
+// of the full tiles, with 16-byte loads, LDS reads and stores, measured no faster: the kernel
+// moves about 4 TB/s of reads and writes either way.)
 constexpr int kPoolTile = 4096;
+constexpr int kPoolMinTile = 256;
+constexpr long long kPoolFillBlocks = 1024;
 constexpr int kPoolHalo = 64;          // largest k/2 served from LDS (k <= 129); larger k reads HBM
 template <int KT>
 __global__ __launch_bounds__(256) void avg_pool_kernel(const float* s, long long rs, int m, int k,
-                                                       long long blocks_per_row, float* out) {
+                                                       long long blocks_per_row, int ntile, float* out) {
   __shared__ float tile[kPoolTile + 2 * kPoolHalo];
   const long long row = (long long)blockIdx.x / blocks_per_row;
-  const int i0 = (int)(((long long)blockIdx.x - row * blocks_per_row) * kPoolTile);
+  const int i0 = (int)(((long long)blockIdx.x - row * blocks_per_row) * ntile);
   const float* x = s + row * rs;
   if (KT > 0) k = KT;
   const int half = k >> 1;
   float* o = out + row * (long long)m;
   if (half <= kPoolHalo) {
-    const int span = min(kPoolTile, m - i0) + 2 * half;
+    const int span = min(ntile, m - i0) + 2 * half;
     for (int t = threadIdx.x; t < span; t += 256) {
       const int j = i0 - half + t;
       tile[t] = (j >= 0 && j < m) ? x[j] : 0.f;
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < kPoolTile; t += 256) {
+    for (int t = threadIdx.x; t < ntile; t += 256) {
       const int i = i0 + t;
       if (i >= m) break;
       // left to right over the window; the zero padding adds exact zeros
@@ -501,7 +505,7 @@ __global__ __launch_bounds__(256) void avg_pool_kernel(const float* s, long long
       o[i] = acc / (float)k;
     }
   } else {
-    for (int t = threadIdx.x; t < kPoolTile; t += 256) {
+    for (int t = threadIdx.x; t < ntile; t += 256) {
       const int i = i0 + t;
       if (i >= m) break;
       const int lo = i - half < 0 ? 0 : i - half;
@@ -946,7 +950,9 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
       set_error("fe_select: pooling needs a workspace of fe_select_workspace_bytes() bytes");
       return FE_ERR_WORKSPACE;
     }
-    const long long bpr = (m + kPoolTile - 1) / kPoolTile;
+    int ntile = kPoolTile;
+    while (ntile > kPoolMinTile && rows * ((m + ntile - 1) / ntile) < kPoolFillBlocks) ntile /= 2;
+    const long long bpr = (m + ntile - 1) / ntile;
     if (bpr * rows > 0x7fffffffLL) {
       set_error("fe_select: pooling grid too large");
       return FE_ERR_UNSUPPORTED;
@@ -960,7 +966,7 @@ extern "C" int fe_select(const float* scores, int64_t rows, int64_t n, int64_t r
     long long rs_arg = src_stride, bpr_arg = bpr;
     const float* s_arg = scores;
     float* o_arg = (float*)workspace;
-    void* pargs[] = {&s_arg, &rs_arg, &m_arg, &k_arg, &bpr_arg, &o_arg};
+    void* pargs[] = {&s_arg, &rs_arg, &m_arg, &k_arg, &bpr_arg, &ntile, &o_arg};
     hipError_t err = hipLaunchKernel(pool_fn, dim3((unsigned)(bpr * rows)), dim3(256), pargs, 0, stream);
     if (err == hipSuccess) err = hipGetLastError();
     if (err != hipSuccess) {
