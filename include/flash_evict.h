@@ -81,13 +81,18 @@ int fe_prefill(const void* q, const void* k, const void* v, void* out, float* im
 int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
 
 /*
- * fe_prefill with a caller-provided workspace (same contract and results up to FP32
- * atomic order). With at least fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
+ * fe_prefill with a caller-provided workspace (same contract). With at least
+ * fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
  * score != 0, else 0) and the fast layouts (D a multiple of 8 up to 256, nonzero scale, unit-stride
  * 16-byte aligned K/V rows; Q of any strides),
  * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
- * per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace. With less
- * workspace (or NULL) this is fe_prefill. Same reference interface as fe_prefill.
+ * per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace. At head dims
+ * 72..128 (multiples of 8) its attention kernel holds two row tiles per wave and takes a row's
+ * reference max over its first 32 keys instead of 64: the output then agrees with fe_prefill's
+ * to within two roundings of the probabilities, the importance to FP32 summation order; at
+ * other head dims the output is bitwise equal and the importance equal up to FP32 atomic
+ * order. With less workspace (or NULL) this is fe_prefill. Same reference interface as
+ * fe_prefill.
  */
 size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score);
 int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance,
