@@ -812,7 +812,12 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       pb[c2] = (u32x4){E::pack2(S[8 * c2 + 0], S[8 * c2 + 1]), E::pack2(S[8 * c2 + 2], S[8 * c2 + 3]),
                        E::pack2(S[8 * c2 + 4], S[8 * c2 + 5]), E::pack2(S[8 * c2 + 6], S[8 * c2 + 7])};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pr[e] = E::sum2(pb[1][e], ones2, E::sum2(pb[0][e], ones2, 0.f));
+    for (int e = 0; e < 4; ++e) {
+      // the zero-accumulator VOP3P form saves a v_mov per chain; measured 1-2% faster on the
+      // common path, 1.5% slower in the replay-row variant (the compiler schedules it worse)
+      const float first = EXACT ? E::sum2(pb[0][e], ones2, 0.f) : E::sum2_0(pb[0][e], ones2);
+      pr[e] = E::sum2(pb[1][e], ones2, first);
+    }
     if constexpr (EXACT)
       return (ps[0] + ps[1]) + (ps[2] + ps[3]);
     else

@@ -43,6 +43,13 @@ struct BF16 {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), __builtin_bit_cast(bf16x2, ones2), acc,
                                            false);
   }
+  // lo + hi of a packed pair (sum2 with acc = 0) as one VOP3P v_dot2_f32_bf16 with an inline
+  // zero: sum2(p, ones2, 0.f) compiles to the accumulating v_dot2c form after a v_mov of 0.
+  static __device__ __forceinline__ float sum2_0(u32 packed, u32 ones2) {
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(packed), "s"(ones2));
+    return r;
+  }
 };
 
 struct F16 {
@@ -62,6 +69,11 @@ struct F16 {
   static constexpr u32 kOnes2 = 0x3c003c00u;
   static __device__ __forceinline__ float sum2(u32 packed, u32 ones2, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), __builtin_bit_cast(f16x2, ones2), acc, false);
+  }
+  static __device__ __forceinline__ float sum2_0(u32 packed, u32 ones2) {
+    float r;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(packed), "s"(ones2));
+    return r;
   }
 };
 
