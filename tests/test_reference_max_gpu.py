@@ -1,11 +1,13 @@
 """GPU tests of the attention kernel's reference max and its output normalisation.
 
-The kernel keeps a row's reference max m at the exact max of the row's first key tile and
-moves it only when a tile's probabilities relative to m could overflow (a lane's tile sum
-above 2^32 for bf16, 2^15 for fp16). It divides the output by the sum of the probabilities
+The kernel keeps a row's reference max m at the exact max of the row's first keys (the first
+64-key tile in the fused kernel, the first 32 keys in the split schedule's two-row-tile kernel
+at head dims 72-128) and moves it only when a step's probabilities relative to m could overflow
+(a lane's sum above 2^32 for bf16, 2^15 for fp16). It divides the output by the sum of the probabilities
 exactly as rounded for the P@V product. The reference's kernel (flash_evict/prefill.py:37-60)
 follows the running max exactly instead, so the key that dominates a row enters P@V as 1.0.
-These tests plant such a key after the first tile:
+These tests plant such a key after the first tile, and at key 40 (inside the first 64-key
+tile, after the first 32 keys):
 
   * a jump of ~2^20 (below the guard): the dominant key's probability is far from 1 and is
     rounded to bf16. With the rounded-sum normalisation the output of every dominated row
@@ -54,10 +56,11 @@ def _planted(n, hq, hk, d, dtype, kp, jump_log2, seed):
     return (q[None].to(dtype).cuda(), k[None].to(dtype).cuda(), v[None].to(dtype).cuda())
 
 
+@pytest.mark.parametrize("kp", [300, 40])
 @pytest.mark.parametrize("jump_log2", [24.0, 60.0])
 @pytest.mark.parametrize("use_ws", [True, False])
-def test_dominant_key_after_first_tile_bf16(jump_log2, use_ws):
-    n, hq, hk, d, kp = 1024, 2, 1, 128, 300
+def test_dominant_key_after_first_tile_bf16(jump_log2, use_ws, kp):
+    n, hq, hk, d = 1024, 2, 1, 128
     print("planted dominant key bf16: n=%d kp=%d jump 2^%g use_ws=%s" % (n, kp, jump_log2, use_ws), flush=True)
     q, k, v = _planted(n, hq, hk, d, torch.bfloat16, kp, jump_log2, seed=11)
     out, imp = _run(q, k, v, True, True, 0.0, 0, use_ws=use_ws)
@@ -72,10 +75,11 @@ def test_dominant_key_after_first_tile_bf16(jump_log2, use_ws):
     assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
 
 
+@pytest.mark.parametrize("d,kp", [(64, 700), (128, 700), (128, 40)])
 @pytest.mark.parametrize("jump_log2", [10.0, 30.0])
-def test_dominant_key_after_first_tile_fp16(jump_log2):
-    n, hq, hk, d, kp = 1024, 4, 2, 64, 700
-    print("planted dominant key fp16: n=%d kp=%d jump 2^%g" % (n, kp, jump_log2), flush=True)
+def test_dominant_key_after_first_tile_fp16(jump_log2, d, kp):
+    n, hq, hk = 1024, 4, 2
+    print("planted dominant key fp16: n=%d d=%d kp=%d jump 2^%g" % (n, d, kp, jump_log2), flush=True)
     q, k, v = _planted(n, hq, hk, d, torch.float16, kp, jump_log2, seed=12)
     out, imp = prefill(q, k, v)
     torch.cuda.synchronize()
