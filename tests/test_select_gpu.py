@@ -17,6 +17,9 @@ CASES = [
     (5, 4000, 400, 0, 1, True), (2, 5000, 2500, 100, 3, True), (7, 2049, 2049, 0, 1, False),
     (6, 3000, 1000, 1000, 7, False), (1, 131072, 1024, 64, 1, False), (3, 70000, 17, 5, 9, True),
     (2, 5000, 300, 10, 11, False), (2, 3000, 200, 0, 201, False), (2, 20000, 700, 3, 5, True),
+    # pooling tiles of 1024 and 4096 outputs (the launch halves the tile until the grid has 1024
+    # blocks; the small cases above take 256)
+    (64, 20064, 1000, 64, 5, False), (300, 16448, 500, 64, 3, False),
 ]
 
 
