@@ -434,25 +434,32 @@ __global__ __launch_bounds__(256) void value_l1_scale_kernel(const u16* v, long 
                                                              int D, int vec, float* imp, long long rows) {
   const long long row = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
   const int sub = threadIdx.x & 7;
-  float s = 0.f;
+  float s = 0.f, cur = 0.f;
   if (row < rows) {
+    if (sub == 0) cur = imp[row];
     const long long bh = row / N;
     const int n = (int)(row - bh * N);
     const long long b = bh / Hkv, h = bh - b * Hkv;
     const u16* p = v + b * vs0 + h * vs1 + (long long)n * vs2;
-    for (int d0 = 8 * sub; d0 < D; d0 += 64) {
-      const u32x4 w = load8(p, vs3, d0, D, vec);
+    // channels 8*sub + 64*i (D <= 256): every load is issued before the first is used
+    u32x4 w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 8 * sub + 64 * i;
+      w[i] = d0 < D ? load8(p, vs3, d0, D, vec) : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        s += fabsf(E::to_f32((u16)(w[e] & 0xffffu)));
-        s += fabsf(E::to_f32((u16)(w[e] >> 16)));
+        s += fabsf(E::to_f32((u16)(w[i][e] & 0xffffu)));
+        s += fabsf(E::to_f32((u16)(w[i][e] >> 16)));
       }
-    }
   }
   s += __shfl_xor(s, 1);
   s += __shfl_xor(s, 2);
   s += __shfl_xor(s, 4);
-  if (row < rows && sub == 0) imp[row] *= s;
+  if (row < rows && sub == 0) imp[row] = cur * s;
 }
 
 __global__ __launch_bounds__(256) void zero_f32_kernel(float* p, long long n) {
