@@ -8,6 +8,8 @@
 //     packing), so each K/V tile in LDS serves NW row tiles; waves 0-3 issue the DMA. At
 //     D = 96 and 128 the kernels run 12 waves, three per SIMD; at D = 32 and 64, 8 (two
 //     workgroups per CU); at 160 and 192, 8 (two per SIMD); at 224 and 256, 4 (one per SIMD).
+//     At tile dims 96 and 128 the split schedule's attention-only traversal runs instead
+//     attn_rt2_kernel: eight waves of two row tiles each (see there).
 //   * The K/V buffers hold pairs of 64-key tiles up to tile dim 128 (one barrier per 128
 //     keys), single tiles above it (one barrier per 64 keys).
 //   * K and V tiles (64 keys) go HBM -> LDS with buffer_load ... lds (16 B per lane), no
@@ -595,8 +597,8 @@ __device__ __forceinline__ int lane_now() {
   return l;
 }
 
-// Traversal 1 with two row tiles per wave (attention only: the split schedule, or no
-// importance), tile dims 96 and 128. Eight waves, two per SIMD, each holding the Q fragments
+// Traversal 1 (reference flash_evict/prefill.py:37-60) with two row tiles per wave (attention
+// only: the split schedule, or no importance), tile dims 96 and 128. Eight waves, two per SIMD, each holding the Q fragments
 // and O accumulators of two row tiles, so every K and V^T fragment read from LDS feeds two
 // MFMAs: half the LDS read traffic per MFMA of fused_fast_kernel, whose fragment reads cost
 // more than its exponentials. A 64-key tile runs as two 32-key halves (QK^T, mask,
