@@ -340,7 +340,8 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      pr[j] = E::sum2(pb[0][j], ones2, 0.f);
+      // zero-accumulator VOP3P form on the common path (see attn_rt2_kernel)
+      pr[j] = EXACT ? E::sum2(pb[0][j], ones2, 0.f) : E::sum2_0(pb[0][j], ones2);
 #pragma unroll
       for (int c = 1; c < 4; ++c) pr[j] = E::sum2(pb[c][j], ones2, pr[j]);
     }
