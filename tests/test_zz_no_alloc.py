@@ -51,9 +51,11 @@ def _run(q, k, v, causal, weighted, decay, window, static):
 @pytest.mark.gpu
 def test_static_entry_matches_workspace_entry_on_two_calls():
     cases = [
-        # larger call first, then a smaller one (fewer rows, another dtype and head dim)
+        # larger call first, then smaller ones (fewer rows, another dtype and head dim; D = 120 runs
+        # the two-row-tile attention kernel below its tile dim)
         ((1, 32, 8, 4096, 128, torch.bfloat16, 20261201), dict(causal=True, weighted=True, decay=0.0, window=0)),
         ((2, 8, 2, 1000, 64, torch.float16, 20261202), dict(causal=True, weighted=True, decay=0.05, window=0)),
+        ((1, 8, 2, 777, 120, torch.bfloat16, 20261203), dict(causal=True, weighted=True, decay=0.0, window=300)),
     ]
     for (b, hq, hk, n, d, dt, seed), kw in cases:
         print("fe_prefill_static vs fe_prefill_ws: B=%d Hq=%d Hkv=%d N=%d D=%d %s %s" % (b, hq, hk, n, d, dt, kw),
@@ -68,8 +70,8 @@ def test_static_entry_matches_workspace_entry_on_two_calls():
 
 
 @pytest.mark.gpu
-def test_static_entry_without_score_and_on_the_generic_path():
-    """score=0 needs no buffer; D=96 takes the generic fused kernel (no split schedule)."""
+def test_static_entry_without_score_and_at_head_dim_96():
+    """score=0 needs no buffer; D=96 runs the split schedule's two-row-tile kernel at tile dim 96."""
     q = seeded_randn((1, 4, 300, 96), torch.bfloat16, 11)
     k = seeded_randn((1, 2, 300, 96), torch.bfloat16, 12)
     v = seeded_randn((1, 2, 300, 96), torch.bfloat16, 13)
