@@ -2,7 +2,9 @@
 
 Each case draws its shape and options from a seeded generator: batch, KV heads and GQA group
 (1, 2, 4 or 7), N from 1 to 700 (tile edges included), head dims 16..256 (the fast kernels for
-multiples of 8 up to 128, on full and partial tiles; the generic kernel above 128 and for 100), fp16/bf16, causal or not, softmax scale (default, small, negative), recency decay
+multiples of 8 up to 256, on full and partial tiles, with the two-row-tile attention kernel at
+72..128; the generic kernel for 100), fp16/bf16, causal or not, softmax scale (default, small,
+negative), recency decay
 (including decays large enough that the replay keeps only a few rows), observation window,
 value weighting, contiguous or transposed layouts, and a selection budget, reserved suffix and
 pool kernel. The attention output and importance are compared with the dense FP32 oracle
