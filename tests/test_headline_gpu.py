@@ -16,7 +16,8 @@ reference's materialized path, flash_evict/reference.py:5-25), run in float32 on
     importance tolerance; the evict mask is the complement of the kept indices.
 
 The same seeded workload with decay 0 (every row replayed: bench.py's full-replay record)
-is checked the same way, its importance against the full-row oracle.
+is checked the same way, its importance against the full-row oracle; and the headline shape
+in fp16 (the f16 kernels, whose overflow guard is 2^15), output within the fp16 bar 5e-3.
 """
 import pytest
 import torch
@@ -32,13 +33,13 @@ B, HQ, HKV, N, D = 1, 32, 8, 32768, 128
 SEED = 20260910          # bench.py's generator seed
 
 
-def _bench_inputs():
+def _bench_inputs(dtype=torch.bfloat16):
     """q, k, v exactly as bench.py draws them (device generator, same order)."""
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev).manual_seed(SEED)
-    q = torch.randn((B, HQ, N, D), device=dev, dtype=torch.bfloat16, generator=gen)
-    k = torch.randn((B, HKV, N, D), device=dev, dtype=torch.bfloat16, generator=gen)
-    v = torch.randn((B, HKV, N, D), device=dev, dtype=torch.bfloat16, generator=gen)
+    q = torch.randn((B, HQ, N, D), device=dev, dtype=dtype, generator=gen)
+    k = torch.randn((B, HKV, N, D), device=dev, dtype=dtype, generator=gen)
+    v = torch.randn((B, HKV, N, D), device=dev, dtype=dtype, generator=gen)
     return q, k, v
 
 
@@ -98,3 +99,30 @@ def test_headline_full_replay_matches_oracle():
     with torch.inference_mode():
         out_ns, _ = flash_evict.prefill(q, k, v, score=False)
     assert torch.equal(out, out_ns)
+
+
+def test_headline_shape_fp16_matches_oracle():
+    """The headline shape and arguments in fp16: the f16 instantiations of the attention,
+    replay and selection kernels at full size."""
+    print("headline shape fp16: decay 0.1, budget 1024, recent 64", flush=True)
+    q, k, v = _bench_inputs(torch.float16)
+    budget, recent, decay = 1024, 64, 0.1
+    with torch.inference_mode():
+        out, imp, idx, evicted = flash_evict.evict(q, k, v, budget, reserved_recent=recent, pool_kernel=1,
+                                                   recency_decay=decay, observation_window=0)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    assert torch.isfinite(out).all() and torch.isfinite(imp).all()
+    _, ref_imp = chunked(q, k, v, block=1100, want_out=False, recency_decay=decay, query_rows=[(N - 1100, N)])
+    rel = assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    print("importance element-wise max rel err %.3e" % rel, flush=True)
+    worst = out_err_all_rows(out, q, k, v)
+    print("out max-abs-err over all %d rows x %d heads: %.4f" % (N, HQ, worst), flush=True)
+    assert worst <= 5e-3
+    _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), budget, reserved_recent=recent)
+    keep = ~evicted
+    assert_same_selection(keep, torch.from_numpy(ref_keep), ref_imp.cpu(), budget, recent, rtol=1e-3)
+    assert keep.sum(-1).eq(budget).all() and keep[..., -recent:].all()
+    oidx, okeep = osel.select_tokens(imp.cpu().numpy(), budget, reserved_recent=recent)
+    assert torch.equal(idx.cpu(), torch.from_numpy(oidx))
+    assert torch.equal(keep.cpu(), torch.from_numpy(okeep))
