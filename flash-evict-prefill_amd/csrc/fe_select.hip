@@ -68,6 +68,7 @@ constexpr int kSegs = 512, kSegLen = 8;            // sample of the long-row sch
 constexpr int kSamples = kSegs * kSegLen;
 constexpr int kCandMax = 12288;                    // (key, index) candidates held in LDS
 constexpr int kBitRowMax = 262144;                 // longest row of the sampled schedule (32 KiB bitmap)
+constexpr int kTieList = 64;                       // ties at the threshold listed in LDS (more: radix select)
 
 // The selection kernels synchronise through LDS with lds_barrier() (fe_common.h):
 // __syncthreads() also waits for every outstanding global load and store of the wave, which
@@ -604,7 +605,9 @@ __global__ __launch_bounds__(kSelThreads) void select_lds_kernel(const float* sr
 // of 16 keys, records their kept bits in an LDS bitmap (one 16-bit word per chunk), counts
 // them, and appends its candidates to the LDS pool at a slot its wave reserves with one LDS
 // atomic. Candidates land in no particular order; ties at the threshold are then broken by
-// index with a second radix select over the tied candidates' indices. The ascending kept
+// index: up to kTieList tied candidates are listed and ranked by index directly (a second
+// radix select over the indices took 6 us of a 42 us row), more by a second radix select
+// over the tied candidates' indices. The ascending kept
 // indices come from one ordered pass over the bitmap (a single block prefix sum). Rows the
 // bitmap cannot hold, and brackets that miss, take the radix passes over HBM.
 __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float* src, long long src_stride, int m,
@@ -824,17 +827,37 @@ __global__ __launch_bounds__(kSelThreads) void select_sample_kernel(const float*
       auto c_key = [&](int j) { return ckey[j]; };
       radix_select(c_key, n_cand, K2, c_lo, c_hi, hist, scan_tmp, &sh, T, need, eq);
       const bool all_eq = eq == need;
-      if (!all_eq) {
-        // ties at T: the `need` lowest indices among them, i.e. the largest ~index
+      // ties at T keep the `need` lowest indices among them. A few ties (the usual case)
+      // are listed in LDS and each tied candidate counts the listed indices below its own;
+      // many take a radix select over ~index (the `need` largest).
+      const bool tie_list = !all_eq && eq <= kTieList;
+      int* tie_idx = (int*)hist;                 // free: radix_select's reads of hist are behind its last barrier
+      if (tie_list) {
+        if (tid == 0) n_cand_lds = 0;            // every thread read n_cand before radix_select's barriers
+        lds_barrier();
+        for (int j = tid; j < n_cand; j += ST) {
+          if (ckey[j] == T) {
+            const int s = atomicAdd(&n_cand_lds, 1);
+            if (s < kTieList) tie_idx[s] = cidx[j];
+          }
+        }
+        lds_barrier();
+      } else if (!all_eq) {
         auto tie_key = [&](int j) { return ckey[j] == T ? ~(u32)cidx[j] : 0u; };
         int need2, eq2;
         radix_select(tie_key, n_cand, need, 0u, 0xffffffffu, hist, scan_tmp, &sh, T2, need2, eq2);
       }
+      auto tie_kept = [&](int ci) -> bool {
+        if (!tie_list) return ~(u32)ci >= T2;
+        int below = 0;
+        for (int t = 0; t < eq; ++t) below += tie_idx[t] < ci ? 1 : 0;
+        return below < need;
+      };
       u32* bits = work;
       for (int j = tid; j < n_cand; j += ST) {
         const u32 key = ckey[j];
         const int ci = cidx[j];
-        if (key > T || (key == T && (all_eq || ~(u32)ci >= T2))) {
+        if (key > T || (key == T && (all_eq || tie_kept(ci)))) {
           atomicOr(&bits[ci >> 5], 1u << (ci & 31));
           if (mrow) mrow[ci] = keep_v;
         }

@@ -114,6 +114,27 @@ def test_sampled_schedule_ties_at_threshold(n):
         _host_equal(x, budget, recent)
 
 
+@pytest.mark.parametrize("n,n_tied", [(70000, 5), (70000, 64), (131072, 65), (131072, 9)])
+def test_sampled_schedule_few_ties_at_threshold(n, n_tied):
+    """Distinct scores except n_tied equal ones straddling the budget: 3 of them rank inside
+    it, so the 3 lowest-index copies are kept. Up to 64 tied candidates are ranked by index
+    from an LDS list, more by a radix select over their indices."""
+    print(f"select few ties n={n} tied={n_tied}", flush=True)
+    g = torch.Generator().manual_seed(n + n_tied)
+    recent = 64
+    budget = 1024
+    K = budget - recent
+    x = torch.randperm(n, generator=g).float() / n                # distinct scores
+    past = x[: n - recent]
+    order = past.argsort(descending=True)
+    tied = order[K - 3: K - 3 + n_tied]                            # ranks K-3 .. K-4+n_tied
+    past[tied] = past[order[K - 1]].item()
+    _host_equal(x.unsqueeze(0).repeat(2, 1), budget, recent)
+    idx_h, _ = select_tokens(x.unsqueeze(0), budget, recent=recent)
+    kept_tied = sorted(set(idx_h[0].tolist()) & set(tied.tolist()))
+    assert kept_tied == sorted(tied.tolist())[:3]
+
+
 def test_sampled_schedule_denormals_and_zeros():
     """Long rows whose threshold falls among FP32 denormals and signed zeros: the sampled
     schedule classifies by float compares, which must order denormals and tie -0 with +0."""
