@@ -28,8 +28,22 @@ struct AttnArgs {
   int neg_scale;
   int causal, score, win_lo;        // win_lo = N - W
   int rsplit;                       // replay kernel: key splits per workgroup of row tiles
+  int* queue;                       // dynamic schedule: item counter, zero at launch (else null)
+  int nitems;                       // dynamic schedule: work items of the launch
+  int nstatic;                      // dynamic schedule: workgroups launched (each starts with item blockIdx.x)
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
 };
+
+// Work-item counters of the dynamic schedule, at the end of the prefill workspace (the
+// next 256-byte boundary after the replay biases): eight per kernel (one per XCD queue), each
+// on its own 128-byte line, the attention kernel's from word 0 and the replay kernel's from
+// word kQueueReplay. Zeroed before every launch.
+constexpr int kQueueStride = 32;
+constexpr int kQueueReplay = 8 * kQueueStride;
+constexpr int kQueueWords = 2 * kQueueReplay;
+constexpr size_t kQueueBytes = kQueueWords * sizeof(int);
+// s_getreg_b32 operand of hwreg(HW_REG_XCC_ID): register 20, bits 0-31 (the XCC index is bits 0-3)
+constexpr int kHwRegXccId = (31 << 11) | 20;
 
 // Load 8 consecutive channels [d0, d0+8) of one row; zero beyond D.
 __device__ __forceinline__ u32x4 load8(const u16* row, long long sd, int d0, int D, int vec) {

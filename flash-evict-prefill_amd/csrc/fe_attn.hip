@@ -462,18 +462,60 @@ __global__ __launch_bounds__(256) void value_l1_scale_kernel(const u16* v, long 
   if (row < rows && sub == 0) imp[row] = cur * s;
 }
 
-__global__ __launch_bounds__(256) void zero_f32_kernel(float* p, long long n) {
+// Zero n floats at p and nc 32-bit words at c (the work-item counters of the dynamic
+// schedule), in one launch.
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* p, long long n, int* c, int nc) {
   const long long stride = (long long)gridDim.x * 256;
-  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+  const long long i0 = (long long)blockIdx.x * 256 + threadIdx.x;
+  for (long long i = i0; i < n; i += stride) p[i] = 0.f;
+  for (long long i = i0; i < nc; i += stride) c[i] = 0;
 }
 
-hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
+hipError_t launch_zero(float* p, int64_t n, int* ctr, int nctr, hipStream_t stream) {
+  if (n <= 0 && nctr <= 0) return hipSuccess;
   long long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, (long long)n);
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, (long long)(n > 0 ? n : 0), ctr,
+                     nctr);
   return hipGetLastError();
 }
+
+hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream) { return launch_zero(p, n, nullptr, 0, stream); }
+
+namespace {
+
+// Workgroups of a kernel that the device holds at once: the CU count times the kernel's
+// occupancy, looked up once per device and kernel.
+std::mutex g_res_mu;
+std::vector<std::pair<std::pair<int, const void*>, int64_t>> g_res;   // ((device, kernel), workgroups)
+
+hipError_t resident_blocks(const void* fn, int threads, size_t lds, hipStream_t stream, int64_t* out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (stream) {
+    hipDevice_t d = 0;
+    if ((err = hipStreamGetDevice(stream, &d)) != hipSuccess) return err;
+    dev = (int)d;
+  }
+  std::lock_guard<std::mutex> lock(g_res_mu);
+  for (const auto& e : g_res)
+    if (e.first.first == dev && e.first.second == fn) {
+      *out = e.second;
+      return hipSuccess;
+    }
+  int cus = 0, per_cu = 0;
+  if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return err;
+  if ((err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds)) != hipSuccess) return err;
+  const int64_t blocks = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+  g_res.push_back({{dev, fn}, blocks});
+  *out = blocks;
+  return hipSuccess;
+}
+
+}  // namespace
+
 
 namespace {
 
@@ -579,6 +621,13 @@ namespace fe {
 // column; the replay's own term exp2(s*scale*log2e - b_q) is bounded by
 // 2^(-decay*log2e*t) <= 2^-151.4 there and underflows to 0 as well. Rows with t < 105/decay
 // are kept: ceil(105/decay) of them, or all `window` rows when that is fewer.
+// Workgroups launched for `items` work items of a kernel that runs one item per workgroup
+// under the dynamic schedule (the replay kernel): one eighth more, rounded up to the 8 XCDs
+// the hardware deals workgroups over in turn, so that an XCD that runs faster than the others
+// can start more than its eighth of them. The workgroups that find every item taken exit at
+// once.
+int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64_t)7); }
+
 int64_t replay_rows(int64_t N, int64_t window, float recency_decay) {
   if (!(recency_decay > 0.f)) return window;
   const double span = ceil(105.0 / (double)recency_decay);
@@ -632,6 +681,9 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.imp = importance;
   a.bias = nullptr;
   a.rsplit = 1;
+  a.queue = nullptr;
+  a.nitems = 0;
+  a.nstatic = 0;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -660,18 +712,28 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
 
   FusedPlan plan;
   ReplayPlan rplan;
-  const size_t ws_need = (size_t)(B * Hq * N) * sizeof(float);
-  const bool split = score && workspace && workspace_bytes >= ws_need && replay_plan(a, dtype, rplan);
+  // Workspace: the replay bias of every query row (scoring calls), then the dynamic
+  // schedule's item counters at the next 256-byte boundary.
+  const size_t ws_bias = score ? (size_t)(B * Hq * N) * sizeof(float) : 0;
+  const size_t ws_ctr = (ws_bias + 255) & ~(size_t)255;
+  const bool split = score && workspace && workspace_bytes >= ws_bias && replay_plan(a, dtype, rplan);
   if (split) a.bias = (float*)workspace;
-  if (!fast_plan(a, dtype, plan)) {
+  bool fast = fast_plan(a, dtype, plan);
+  if (!fast) {
     int dpi = 0;
     while (dpi < kNumDP - 1 && kDP[dpi] < D) ++dpi;
     const FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
     plan = FusedPlan{(const void*)ent.fn, ent.lds, 4, 4, ent.name};
   }
+  // Dynamic schedule (fast attention-only kernels, and the replay kernel): needs the
+  // counters, i.e. the whole workspace of fe_prefill_workspace_bytes.
+  int* ctr = nullptr;
+  if (fast && (split || !score) && workspace && workspace_bytes >= ws_ctr + kQueueBytes)
+    ctr = (int*)((char*)workspace + ws_ctr);
   // Workgroups are sized by the plan's row tiles per workgroup.
   a.wg_bh = (int)((tiles_bh + plan.rows - 1) / plan.rows);
-  const int64_t grid = B * Hkv * (int64_t)a.wg_bh;
+  const int64_t items = B * Hkv * (int64_t)a.wg_bh;
+  int64_t grid = items;
 
   hipStream_t stream = (hipStream_t)hip_stream;
   hipError_t err = prepare_plan(plan);
@@ -679,8 +741,19 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
     return FE_ERR_HIP;
   }
-  if (score) {
-    err = launch_zero_f32(importance, B * Hkv * N, stream);
+  if (ctr) {
+    int64_t resident = 0;
+    if ((err = resident_blocks(plan.fn, 64 * plan.waves, plan.lds, stream, &resident)) != hipSuccess) {
+      set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+    a.queue = ctr;
+    a.nitems = (int)items;
+    a.nstatic = (int)(items < resident ? items : resident);
+    grid = a.nstatic;
+  }
+  if (score || ctr) {
+    err = launch_zero(score ? importance : nullptr, score ? B * Hkv * N : 0, ctr, ctr ? kQueueWords : 0, stream);
     if (err != hipSuccess) {
       set_error(std::string("fe_prefill: zero-init launch: ") + hipGetErrorString(err));
       return FE_ERR_HIP;
@@ -723,7 +796,18 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     int64_t rs = (1024 + nwg - 1) / nwg;
     rs = rs < 1 ? 1 : (rs > max_tiles ? max_tiles : rs);
     r.rsplit = (int)rs;
-    const int64_t rgrid = nwg * rs;
+    int64_t rgrid = nwg * rs;
+    if (ctr) {
+      int64_t resident = 0;
+      if ((err = resident_blocks(rplan.fn, 64 * rplan.waves, 0, stream, &resident)) != hipSuccess) {
+        set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
+        return FE_ERR_HIP;
+      }
+      r.queue = ctr + kQueueReplay;
+      r.nitems = (int)rgrid;
+      r.nstatic = (int)(rgrid < resident ? rgrid : resident);
+      rgrid = one_shot_grid(rgrid);
+    }
     void* rargs[] = {&r};
     err = hipLaunchKernel(rplan.fn, dim3((unsigned)rgrid), dim3(64 * rplan.waves), rargs, 0, stream);
     if (err != hipSuccess) {
@@ -776,8 +860,9 @@ extern "C" int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay
 }
 
 extern "C" size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score) {
-  if (!score || B < 1 || Hq < 1 || N < 1) return 0;
-  return (size_t)(B * Hq * N) * sizeof(float);
+  if (B < 1 || Hq < 1 || N < 1) return 0;
+  const size_t bias = score ? (size_t)(B * Hq * N) * sizeof(float) : 0;
+  return ((bias + 255) & ~(size_t)255) + kQueueBytes;
 }
 
 extern "C" int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
@@ -793,11 +878,13 @@ extern "C" int fe_prefill_ws(const void* q, const void* k, const void* v, void* 
 namespace fe {
 namespace {
 
-// Replay-bias buffer of fe_prefill_static: a file-scope device array, so that entry point
-// allocates nothing. FE_STATIC_BIAS_ROWS floats (16 MiB) on every GPU the library runs on,
-// held until the process ends. Its contents persist between calls (the last call's biases);
-// the attention kernel writes every bias the replay kernel reads, so nothing is cleared.
-__device__ __align__(256) float scratch[FE_STATIC_BIAS_ROWS];
+// Workspace of fe_prefill_static: a file-scope device array, so that entry point allocates
+// nothing. FE_STATIC_BIAS_ROWS floats of replay biases plus the dynamic schedule's item
+// counters (16 MiB + 256 B) on every GPU the library runs on, held until the process ends.
+// Its contents persist between calls (the last call's biases and counters); the attention
+// kernel writes every bias the replay kernel reads, and each call zeroes the counters (with
+// a fill kernel) before its kernels run.
+__device__ __align__(256) float scratch[FE_STATIC_BIAS_ROWS + kQueueWords];
 
 // Device address of `scratch`, per device: looked up once per device, with that device
 // current, on the first fe_prefill_static call that runs on it. Host code passes this
@@ -847,9 +934,9 @@ extern "C" int fe_prefill_static(const void* q, const void* k, const void* v, vo
   clear_error();
   float* ws = nullptr;
   size_t ws_bytes = 0;
-  if (score && B >= 1 && Hq >= 1 && N >= 1) {
+  if (B >= 1 && Hq >= 1 && N >= 1) {
     const int64_t R = FE_STATIC_BIAS_ROWS;
-    if (B > R || Hq > R || N > R || B * Hq > R || B * Hq * N > R) {
+    if (score && (B > R || Hq > R || N > R || B * Hq > R || B * Hq * N > R)) {
       char msg[256];
       snprintf(msg, sizeof(msg),
                "fe_prefill_static: B*Hq*N = %.0f query rows exceed the static replay-bias buffer of %lld rows; "
@@ -863,7 +950,7 @@ extern "C" int fe_prefill_static(const void* q, const void* k, const void* v, vo
       set_error(std::string("fe_prefill_static: static buffer lookup: ") + hipGetErrorString(err));
       return FE_ERR_HIP;
     }
-    ws_bytes = (size_t)(B * Hq * N) * sizeof(float);
+    ws_bytes = fe_prefill_workspace_bytes(B, Hq, N, score);
   }
   return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
                       causal, value_weighted, score, recency_decay, window, ws, ws_bytes, hip_stream,

@@ -118,6 +118,97 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
   }
 }
 
+// The lane's index, recomputed where it is used: opaque to the compiler, which would
+// otherwise keep values derived from it live across a loop and, at two or three waves per
+// SIMD, spill them (each reload then waits behind the next tile's DMA).
+__device__ __forceinline__ int lane_now() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// Work items. Without a queue a workgroup runs the one item blockIdx.x. The dynamic schedule
+// launches as many workgroups as the chip holds at once (a.nstatic) and each loops over items:
+// its first is blockIdx.x, and the hardware deals those over the XCDs in turn (workgroup b to
+// XCD b % 8) and over each XCD's CUs in order, so no CU starts with several of the heaviest
+// items. Items are numbered heaviest first, with consecutive numbers on different KV heads,
+// and the rest are dealt to eight queues, one per XCD: queue x holds items x, x + 8, x + 16,
+// ... past the first ones (with B*Hkv a multiple of 8, the KV heads h with h % 8 == x, whose
+// K/V tiles that XCD's L2 then serves). A workgroup takes its next item from its own XCD's
+// queue (hardware register XCC_ID) or, once that is empty, from the next queue with items
+// left, and exits when none has any. So each item goes to whichever CU frees up first within
+// its XCD, without waiting for the hardware dispatcher, which starts workgroups in order and
+// holds a free CU of one XCD until the next workgroup for another XCD has found room; and
+// XCDs that run faster than the others (their clocks differ by several percent under these
+// kernels) take over the lightest items of the slower ones. The barrier before the fetch
+// orders every wave's LDS reads of the previous item (and its read of the shared index)
+// before the next item's first tile DMA and the next index. Returns a block-uniform index.
+// wv is the wave's index in the workgroup (uniform); the lane index is taken opaquely, so
+// nothing lane-derived is hoisted out of the caller's item loop and held across it.
+__device__ __forceinline__ int queue_len(int nitems, int x) { return (nitems - x + 7) >> 3; }
+
+// The next item for a workgroup on XCD x, taken by wave 0 (uniform result; a.nitems when
+// every queue is empty).
+__device__ __forceinline__ int take_item(const AttnArgs& a) {
+  const int lane = lane_now();
+  const int x = (int)(__builtin_amdgcn_s_getreg(kHwRegXccId) & 7u);
+  // the j-th item taken from queue q is its entry queue_len(nstatic, q) + j
+  int got = -1;
+  if (lane == 0) {
+    const int j = queue_len(a.nstatic, x) + atomicAdd(a.queue + kQueueStride * x, 1);
+    if (j < queue_len(a.nitems, x)) got = 8 * j + x;
+  }
+  int item = __shfl(got, 0);
+  // Other queues, nearest first: lanes 0-6 read queues x+1 .. x+7 at once, lane 0 takes from
+  // the first with items left. Each failed take leaves that queue exhausted for good (the
+  // counters only grow), so at most seven rounds run.
+  for (int round = 0; round < 7 && item < 0; ++round) {
+    bool left = false;
+    if (lane < 7) {
+      const int qx = (x + 1 + lane) & 7;
+      left = queue_len(a.nstatic, qx) +
+                 __hip_atomic_load(a.queue + kQueueStride * qx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             queue_len(a.nitems, qx);
+    }
+    const unsigned long long m = __ballot(left);
+    if (m == 0) break;
+    const int qx = (x + __ffsll(m)) & 7;
+    got = -1;
+    if (lane == 0) {
+      const int j = queue_len(a.nstatic, qx) + atomicAdd(a.queue + kQueueStride * qx, 1);
+      if (j < queue_len(a.nitems, qx)) got = 8 * j + qx;
+    }
+    item = __shfl(got, 0);
+  }
+  return item < 0 ? a.nitems : item;
+}
+
+// Item loop of the attention kernels: after the barrier (every wave done with the previous
+// item's LDS tiles and the shared index), wave 0 takes the next item.
+__device__ __forceinline__ int next_item(const AttnArgs& a, int* s_item, int wv) {
+  __syncthreads();
+  if (wv == 0) {
+    const int item = take_item(a);
+    if (lane_now() == 0) *s_item = item;
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*s_item);
+}
+
+// One item per workgroup (the replay kernel, whose tile loop has no registers to spare for
+// an item loop): the first a.nstatic workgroups run item blockIdx.x, the launch has more
+// workgroups than items, and each later one takes an item from the queues when it starts
+// (or exits, finding none).
+__device__ __forceinline__ int block_item(const AttnArgs& a, int* s_item, int wv) {
+  if (!a.queue || (int)blockIdx.x < a.nstatic) return (int)blockIdx.x;
+  if (wv == 0) {
+    const int item = take_item(a);
+    if (lane_now() == 0) *s_item = item;
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*s_item);
+}
+
 // NW waves of one row tile each (8: two waves per SIMD; 12: three, at D = 128, which then
 // reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
@@ -151,452 +242,460 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
   __shared__ float red[FUSED ? 2 * NW * BN : 1];  // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
-  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
-  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
-  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
-  const int t_begin = wg * NW;
-  const int t_end = min(a.tiles_bh, t_begin + NW);
-  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
-  const int kv_end = a.causal ? wg_q_hi : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  __shared__ int s_item;
+  // One work item; `return` ends it.
+  auto run_item = [&](const int item) __attribute__((always_inline)) {
+    const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
+    // The divisors of the item decode, taken opaquely: otherwise the compiler keeps their
+    // reciprocals, computed once before the item loop, in registers across it.
+    int BH = a.BH, G = a.G, Hkv = a.Hkv;
+    asm volatile("" : "+s"(BH), "+s"(G), "+s"(Hkv));
+    const int bh = (int)((unsigned)item % (unsigned)BH);
+    const int wg = a.wg_bh - 1 - (int)((unsigned)item / (unsigned)BH);
+    const int b = bh / Hkv, hkv = bh - b * Hkv;
+    const int t_begin = wg * NW;
+    const int t_end = min(a.tiles_bh, t_begin + NW);
+    const int wg_q_hi = min(N, ((t_end - 1) / G + 1) * 32);
+    const int kv_end = a.causal ? wg_q_hi : N;
+    const int ntiles = (kv_end + BN - 1) / BN;
 
-  // This wave's row tile: 32 query positions from q0 of query head `head`.
-  const int t = t_begin + wv;
-  const bool tv = t < t_end;
-  const int tt = tv ? t : t_begin;
-  const int q0 = (tt / a.G) * 32;
-  const int head = hkv * a.G + (tt - (tt / a.G) * a.G);
-  // last key this lane's query row may see (-1 for a padding tile); the smallest such limit
-  // of the tile (tiles past it are masked) and the largest (tiles past it are skipped)
-  const int qlim = !tv ? -1 : (a.causal ? min(q0 + l32, N - 1) : N - 1);
-  const int lo_lim = !tv ? -1 : (a.causal ? min(q0, N - 1) : N - 1);
-  const int wave_hi = !tv ? -1 : (a.causal ? min(q0 + 31, N - 1) : N - 1);
+    // This wave's row tile: 32 query positions from q0 of query head `head`.
+    const int t = t_begin + wv;
+    const bool tv = t < t_end;
+    const int tt = tv ? t : t_begin;
+    const int q0 = (tt / G) * 32;
+    const int head = hkv * G + (tt - (tt / G) * G);
+    // last key this lane's query row may see (-1 for a padding tile); the smallest such limit
+    // of the tile (tiles past it are masked) and the largest (tiles past it are skipped)
+    const int qlim = !tv ? -1 : (a.causal ? min(q0 + l32, N - 1) : N - 1);
+    const int lo_lim = !tv ? -1 : (a.causal ? min(q0, N - 1) : N - 1);
+    const int wave_hi = !tv ? -1 : (a.causal ? min(q0 + 31, N - 1) : N - 1);
 
-  // A negative scale runs as |scale| on -Q: the sign bits of Q flip at load, and
-  // (-q).k = -(q.k) exactly in the FP32 accumulation, so the logits are those of scale * Q K^T
-  const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
-  u32x4 qf[NDC];
-  {
-    const int qr = q0 + l32;
-    const bool ok = tv && qr < N;
-    const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
-#pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
-  }
-
-  // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
-  // group, buffer and slot enter as instruction immediates.
-  //   K tile: [chunk pair c][64 keys][32 B]. Fragment c of key 32s + l32 is chunk 2c + h
-  //   (h = lane/32) at c*2048 + (32s + l32)*32 + 16*(h ^ key bit 3): the XOR puts keys k and
-  //   k+8 in different halves of the 256-byte bank row, so the 16 lanes of a read phase hit
-  //   every bank once.
-  //   V tile: [channel tile dt][64 keys][64 B], unswizzled: four consecutive keys fill one
-  //   256-byte bank row. The V^T fragment of channel tile dt, 16-key group c4, holds eight
-  //   keys of channel 32dt + lane%32 in P^T slot order: slots 0-3 = keys 4h + 0..3 and slots
-  //   4-7 = keys 8 + 4h + 0..3 (two transposing reads, + 512 B apart).
-  const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
-  u32 voff;
-  {
-    const int r = lane & 15, g = lane >> 4;
-    voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
-  }
-
-  // Per-lane global offsets of the tile DMA (dma_tile_cm), the same for every block and
-  // wave: K blocks are 32 keys x 2 chunks (lane l: key l/2, chunk l%2 XOR key bit 3, the
-  // swizzle above), V blocks 16 keys x 4 chunks (lane l: key l/4, chunk l%4).
-  const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
-  const u32 dk = (u32)(lane >> 1) * krow + (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
-  const u32 dv = (u32)(lane >> 2) * vrow + (u32)((lane & 3) << 4);
-  const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
-  const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
-  // PARTIAL: the lanes' first channel within their K (16-channel) and V (32-channel) group
-  const u32 dchk = (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 3), dchv = (u32)((lane & 3) << 3);
-  auto dma_k = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, dk, kb, N, ldst, wv, a.D, dchk); };
-  auto dma_v = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, dv, kb, N, ldst, wv, a.D, dchv); };
-
-  // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunk pairs h*NDC/KH .. +NDC/KH
-  auto k_frags = [&](int BUF, int SLOT, int s, int h, u32x4(&kf)[NDC / KH]) __attribute__((always_inline)) {
-    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
-#pragma unroll
-    for (int c = 0; c < NDC / KH; ++c) kf[c] = *(const u32x4*)(kt + (h * (NDC / KH) + c) * 2048);
-  };
-  // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT
-  auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
-    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
-    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
-    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
-    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
-    return (u32x4){ux[0], ux[1], uy[0], uy[1]};
-  };
-
-  f32x16 o[NDT];
-  float m_run = NEG_INF;                         // reference max of the row (log2 units)
-  float l_run = 0.f;                             // FP32 sum of the probabilities (replay rows)
-  float l_rnd = 0.f;                             // sum of the probabilities as rounded for P@V
-  float nm = 0.f;                                // -m_run, or 0 while m_run is -inf
-  bool fresh = true;                             // no tile of this row tile seen yet
-  // Only rows the replay visits need the FP32 sum (their replay bias); it is wave-uniform.
-  const bool exact_l = a.score && tv && q0 + 31 >= a.win_lo;
-  u32 ones2;                                     // (1, 1) of the element type, for E::sum2
-  asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
-
-  // ---------------- traversal 1
-  // Tiles are processed in pairs per barrier: buffer BUF holds tiles it and it+1 while the
-  // DMA fills the other buffer with tiles it+2 and it+3.
-  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (dmaw) {
-#pragma unroll
-      for (int sl = 0; sl < SLOTS; ++sl)
-        if (it + SLOTS + sl < ntiles) {
-          dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
-          dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
-        }
-    }
-  };
-  // One 64-key tile: S^T = K Q^T (two 32-key accumulators; lanes hold queries), mask on
-  // diagonal and ragged tiles, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
-  //
-  // Reference max. The row's first tile sets m to its exact max, so that tile's largest
-  // probability is exactly 1 and every row sum is at least 1. Later tiles keep m; their
-  // probabilities may exceed 1 where the row's max has risen. The output is O divided by
-  // l_rnd, the sum of the probabilities exactly as rounded for the P@V product, so a row
-  // dominated by one key returns that key's value whatever m is (dividing by the unrounded
-  // sum would leave that key's rounding error, up to 2^-9 relative in bf16, in the output).
-  // The replay bias needs the FP32 sum of the unrounded probabilities (l_run, replay rows
-  // only): b = m + log2 l_run does not depend on the choice of m. A tile some lane of which
-  // sums to more than E::kMaxTileSum (inf included) takes a new exact max, rescales O and
-  // both sums and recomputes its probabilities, which are then at most 1. For random inputs
-  // that happens on a few percent of tiles, where following the exact running max rescaled
-  // O on ~40% of them, and no tile spends instructions on a row max.
-  auto exact_max = [&](const f32x16(&sacc)[2]) __attribute__((always_inline)) -> float {
-    // max over the 32 keys of this lane and the other half-wave: two chains of three-input
-    // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
-    float mc[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      mc[s] = vmax(vmax(sacc[s][0], sacc[s][1]), sacc[s][2]);
-#pragma unroll
-      for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
-    }
-    return half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15]))) * a.abs_scale_log2;
-  };
-  // S^T of one tile into sacc, masked on diagonal and ragged tiles
-  auto qk_tile = [&](int kb, int BUF, int SLOT, f32x16(&sacc)[2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int h = 0; h < KH; ++h) {
-        u32x4 kf[NDC / KH];
-        k_frags(BUF, SLOT, s, h, kf);
-        FE_PRIO_HI();
-#pragma unroll
-        for (int c = 0; c < NDC / KH; ++c) {
-          const int cc = h * (NDC / KH) + c;
-          sacc[s] = cc == 0 ? E::mfma(kf[c], qf[0], (f32x16){}) : E::mfma(kf[c], qf[cc], sacc[s]);
-        }
-        FE_PRIO_LO();
-      }
-    }
-    if (kb + BN - 1 > lo_lim) {
-      // key kb + 32s + 8(i/4) + 4h + i%4 is visible iff its offset within the tile is at most
-      // rel: one subtraction per lane, then compares against inline constants
-      const int rel = qlim - kb - 4 * hh;
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          sacc[s][i] = 32 * s + 8 * (i >> 2) + (i & 3) <= rel ? sacc[s][i] : NEG_INF;
-    }
-  };
-  // P = exp2(S*scale - m) packed to the input dtype, with per-lane partial sums of the
-  // rounded probabilities (pr). The EXACT flavour (replay rows) also returns the lane's FP32
-  // sum of the unrounded ones. The two flavours are separate code under a wave-uniform
-  // branch: folded into one, the compiler turns the condition into a select per element.
-  // S is consumed in place.
-  auto probs = [&](auto exact_tag, f32x16(&sacc)[2], u32x4(&pb)[4], float(&pr)[4]) __attribute__((always_inline)) {
-    constexpr bool EXACT = decltype(exact_tag)::value;
-    float ps[4];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float p[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nm));
-        if constexpr (EXACT) ps[i & 3] = s == 0 && i < 4 ? p[i] : ps[i & 3] + p[i];
-      }
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2)
-        pb[2 * s + c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
-                                 E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // zero-accumulator VOP3P form on the common path (see attn_rt2_kernel)
-      pr[j] = EXACT ? E::sum2(pb[0][j], ones2, 0.f) : E::sum2_0(pb[0][j], ones2);
-#pragma unroll
-      for (int c = 1; c < 4; ++c) pr[j] = E::sum2(pb[c][j], ones2, pr[j]);
-    }
-    if constexpr (EXACT)
-      return (ps[0] + ps[1]) + (ps[2] + ps[3]);
-    else
-      return 0.f;
-  };
-  auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
-    const int kb = it * BN;
-    if (kb > wave_hi) return;
-
-    f32x16 sacc[2];
-    qk_tile(kb, BUF, SLOT, sacc);
-    if (fresh) {
-      // first tile of the row tile (O and the sums are still zero): exact max, no rescale
-      const float mt = exact_max(sacc);
-      m_run = mt;
-      nm = mt == NEG_INF ? 0.f : -mt;
-      fresh = false;
-    }
-    u32x4 pb[4];
-    float pr[4];
-    float le = probs(exact_tag, sacc, pb, pr);
-    // overflow guard on a lane's tile sum: the FP32 sum where it exists (ready right after the
-    // exponentials), else the rounded one
-    const float guard = decltype(exact_tag)::value ? le : (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    if (__any(guard > E::kMaxTileSum)) {
-      // S again (the tile is still in LDS), the new exact max, O and both sums rescaled,
-      // probabilities recomputed: now all at most 1
-      qk_tile(kb, BUF, SLOT, sacc);
-      const float mt = exact_max(sacc);
-      const float mn = vmax(m_run, mt);
-      const float corr = mn > m_run ? fast_exp2(m_run - mn) : 1.f;
-      l_run *= corr;
-      l_rnd *= corr;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      m_run = mn;
-      nm = mn == NEG_INF ? 0.f : -mn;
-      le = probs(exact_tag, sacc, pb, pr);
-    }
-    l_rnd += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    if constexpr (decltype(exact_tag)::value) l_run += le;
-
-    if constexpr (NW > 8) {
-      // three waves per SIMD cover the V read latency; no prefetch (16 fewer registers)
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        u32x4 vf[4];
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) vf[c4] = v_frag(BUF, SLOT, c4, dt);
-        FE_PRIO_HI();
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[c4], pb[c4], o[dt]);
-        FE_PRIO_LO();
-      }
-    } else {
-      // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
-      u32x4 vf[2][4];
-#pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        if (dt + 1 < NDT) {
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
-        }
-        FE_PRIO_HI();
-#pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[dt & 1][c4], pb[c4], o[dt]);
-        FE_PRIO_LO();
-      }
-    }
-  };
-
-  if (dmaw) {
-#pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl)
-      if (sl < ntiles) {
-        dma_k(sl * BN, lds_k0 + sl * TILE);
-        dma_v(sl * BN, lds_v0 + sl * TILE);
-      }
-  }
-  // The tile loop is instantiated twice, with and without the FP32 sum of the replay rows,
-  // and each wave runs one of them: the choice is made once per wave, not per tile.
-  auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
-    if constexpr (SLOTS == 2) {
-      for (int it = 0; it < ntiles; it += 4) {
-        t1_sync(it, 0);
-        t1_step(exact_tag, it, 0, 0);
-        if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
-        if (it + 2 < ntiles) {
-          t1_sync(it + 2, 1);
-          t1_step(exact_tag, it + 2, 1, 0);
-          if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
-        }
-      }
-    } else {
-      for (int it = 0; it < ntiles; it += 2) {
-        t1_sync(it, 0);
-        t1_step(exact_tag, it, 0, 0);
-        if (it + 1 < ntiles) {
-          t1_sync(it + 1, 1);
-          t1_step(exact_tag, it + 1, 1, 0);
-        }
-      }
-    }
-  };
-  if (exact_l)
-    t1_loop(std::true_type{});
-  else
-    t1_loop(std::false_type{});
-
-  // ---------------- finish rows
-  const float l_tot = half_swap_sum(l_run);      // replay rows only
-  {
-    const int qi = q0 + l32;
-    if (tv && qi < N) {
-      const float inv = 1.f / half_swap_sum(l_rnd);
-      u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * (PARTIAL ? a.D : DP);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d0 = 32 * dt + 8 * g4 + 4 * hh;
-          if (PARTIAL && d0 >= a.D) continue;    // channels past D (a multiple of 8) are not stored
-          const u32 w0 = E::pack2(o[dt][4 * g4 + 0] * inv, o[dt][4 * g4 + 1] * inv);
-          const u32 w1 = E::pack2(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv);
-          *(u32x2*)(op + d0) = (u32x2){w0, w1};
-        }
-      }
-    }
-  }
-
-  // ---------------- traversal 2: replay
-  if (!a.score) return;
-  if (a.bias) {
-    // Split schedule: hand the row's replay bias (see below) to replay_fast_kernel.
-    const int qi = q0 + l32;
-    if (hh == 0 && tv && qi < N) {
-      const bool live = qi >= a.win_lo;
-      a.bias[(long long)(b * a.Hq + head) * N + qi] =
-          live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
-    }
-    return;
-  }
-  if constexpr (FUSED) {
-    if (wg_q_hi - 1 < a.win_lo) return;
-
-    // p_qk * w_q / l_q = exp2(s*scale - b_q) with b_q = m_q + log2 l_q - decay*log2e*(q-N+1),
-    // b_q = +inf for rows outside the window or past N. nb holds -b of the 16 rows of a lane.
-    float nb[16];
+    // A negative scale runs as |scale| on -Q: the sign bits of Q flip at load, and
+    // (-q).k = -(q.k) exactly in the FP32 accumulation, so the logits are those of scale * Q K^T
+    const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
+    u32x4 qf[NDC];
     {
-      const int qi = q0 + l32;
-      const bool live = tv && qi < N && qi >= a.win_lo;
-      const float br = live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+      const int qr = q0 + l32;
+      const bool ok = tv && qr < N;
+      const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
   #pragma unroll
-      for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+      for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     }
-    const bool rin = tv && q0 + 31 >= a.win_lo;
-    const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
-    float* imp_row = a.imp + (long long)bh * N;
 
-    // Flush of the previous tile's per-wave column sums (written before the barrier that
-    // precedes this call): one atomic per key per workgroup.
-    auto flush = [&](int kb_prev, int buf_prev) {
-      if (tid < BN) {
-        const float* rr = red + buf_prev * NW * BN + tid;
-        float sum = 0.f;
+    // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
+    // group, buffer and slot enter as instruction immediates.
+    //   K tile: [chunk pair c][64 keys][32 B]. Fragment c of key 32s + l32 is chunk 2c + h
+    //   (h = lane/32) at c*2048 + (32s + l32)*32 + 16*(h ^ key bit 3): the XOR puts keys k and
+    //   k+8 in different halves of the 256-byte bank row, so the 16 lanes of a read phase hit
+    //   every bank once.
+    //   V tile: [channel tile dt][64 keys][64 B], unswizzled: four consecutive keys fill one
+    //   256-byte bank row. The V^T fragment of channel tile dt, 16-key group c4, holds eight
+    //   keys of channel 32dt + lane%32 in P^T slot order: slots 0-3 = keys 4h + 0..3 and slots
+    //   4-7 = keys 8 + 4h + 0..3 (two transposing reads, + 512 B apart).
+    const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+    u32 voff;
+    {
+      const int r = lane & 15, g = lane >> 4;
+      voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
+    }
+
+    // Per-lane global offsets of the tile DMA (dma_tile_cm), the same for every block and
+    // wave: K blocks are 32 keys x 2 chunks (lane l: key l/2, chunk l%2 XOR key bit 3, the
+    // swizzle above), V blocks 16 keys x 4 chunks (lane l: key l/4, chunk l%4).
+    const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
+    const u32 dk = (u32)(lane >> 1) * krow + (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 4);
+    const u32 dv = (u32)(lane >> 2) * vrow + (u32)((lane & 3) << 4);
+    const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+    const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
+    // PARTIAL: the lanes' first channel within their K (16-channel) and V (32-channel) group
+    const u32 dchk = (u32)(((lane & 1) ^ ((lane >> 4) & 1)) << 3), dchv = (u32)((lane & 3) << 3);
+    auto dma_k = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, dk, kb, N, ldst, wv, a.D, dchk); };
+    auto dma_v = [&](int kb, unsigned char* ldst) { dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, dv, kb, N, ldst, wv, a.D, dchv); };
+
+    // K fragments of keys 32*s + l32 from buffer BUF, slot SLOT: chunk pairs h*NDC/KH .. +NDC/KH
+    auto k_frags = [&](int BUF, int SLOT, int s, int h, u32x4(&kf)[NDC / KH]) __attribute__((always_inline)) {
+      const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
   #pragma unroll
-        for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
-        const int key = kb_prev + tid;
-        if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
-      }
+      for (int c = 0; c < NDC / KH; ++c) kf[c] = *(const u32x4*)(kt + (h * (NDC / KH) + c) * 2048);
+    };
+    // V^T fragment of channel tile dt, 16-key group c4, buffer BUF, slot SLOT
+    auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
+      const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
+      const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
+      const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
+      const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+      return (u32x4){ux[0], ux[1], uy[0], uy[1]};
     };
 
-    // One 64-key tile: S = Q K^T (lanes hold keys), causal mask on diagonal tiles, column
-    // sums of exp2(S*scale - b_q) over this wave's 32 rows, written to LDS for the flush.
-    auto t2_step = [&](int it, int BUF) __attribute__((always_inline)) {
-      const int kb = it * BN;
+    f32x16 o[NDT];
+    float m_run = NEG_INF;                         // reference max of the row (log2 units)
+    float l_run = 0.f;                             // FP32 sum of the probabilities (replay rows)
+    float l_rnd = 0.f;                             // sum of the probabilities as rounded for P@V
+    float nm = 0.f;                                // -m_run, or 0 while m_run is -inf
+    bool fresh = true;                             // no tile of this row tile seen yet
+    // Only rows the replay visits need the FP32 sum (their replay bias); it is wave-uniform.
+    const bool exact_l = a.score && tv && q0 + 31 >= a.win_lo;
+    u32 ones2;                                     // (1, 1) of the element type, for E::sum2
+    asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
+  #pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = (f32x16){};
+
+    // ---------------- traversal 1
+    // Tiles are processed in pairs per barrier: buffer BUF holds tiles it and it+1 while the
+    // DMA fills the other buffer with tiles it+2 and it+3.
+    auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (it > 0) flush(kb - BN, BUF ^ 1);
-      if (dmaw && it + 1 < ntiles) dma_k(kb + BN, BUF == 0 ? lds_k1 : lds_k0);
-      float cs[2] = {0.f, 0.f};
-      if (kb <= wave_hi_r) {
-        f32x16 sacc[2];
+      if (dmaw) {
   #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-  #pragma unroll
-          for (int h = 0; h < KH; ++h) {
-            u32x4 kf[NDC / KH];
-            k_frags(BUF, 0, s, h, kf);
-            FE_PRIO_HI();
-  #pragma unroll
-            for (int c = 0; c < NDC / KH; ++c) {
-              const int cc = h * (NDC / KH) + c;
-              sacc[s] = cc == 0 ? E::mfma(qf[0], kf[c], (f32x16){}) : E::mfma(qf[cc], kf[c], sacc[s]);
-            }
-            FE_PRIO_LO();
+        for (int sl = 0; sl < SLOTS; ++sl)
+          if (it + SLOTS + sl < ntiles) {
+            dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+            dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
           }
-        }
-        if (a.causal && kb + BN - 1 > q0) {
+      }
+    };
+    // One 64-key tile: S^T = K Q^T (two 32-key accumulators; lanes hold queries), mask on
+    // diagonal and ragged tiles, P = exp2(S*scale - m) rounded to the input dtype, O^T += V^T P^T.
+    //
+    // Reference max. The row's first tile sets m to its exact max, so that tile's largest
+    // probability is exactly 1 and every row sum is at least 1. Later tiles keep m; their
+    // probabilities may exceed 1 where the row's max has risen. The output is O divided by
+    // l_rnd, the sum of the probabilities exactly as rounded for the P@V product, so a row
+    // dominated by one key returns that key's value whatever m is (dividing by the unrounded
+    // sum would leave that key's rounding error, up to 2^-9 relative in bf16, in the output).
+    // The replay bias needs the FP32 sum of the unrounded probabilities (l_run, replay rows
+    // only): b = m + log2 l_run does not depend on the choice of m. A tile some lane of which
+    // sums to more than E::kMaxTileSum (inf included) takes a new exact max, rescales O and
+    // both sums and recomputes its probabilities, which are then at most 1. For random inputs
+    // that happens on a few percent of tiles, where following the exact running max rescaled
+    // O on ~40% of them, and no tile spends instructions on a row max.
+    auto exact_max = [&](const f32x16(&sacc)[2]) __attribute__((always_inline)) -> float {
+      // max over the 32 keys of this lane and the other half-wave: two chains of three-input
+      // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
+      float mc[2];
   #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            // key kb + 32s + l32 against row q0 + 8(i/4) + 4h + i%4
-            const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+      for (int s = 0; s < 2; ++s) {
+        mc[s] = vmax(vmax(sacc[s][0], sacc[s][1]), sacc[s][2]);
   #pragma unroll
-            for (int i = 0; i < 16; ++i) sacc[s][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[s][i];
+        for (int i = 3; i < 15; i += 2) mc[s] = vmax(vmax(mc[s], sacc[s][i]), sacc[s][i + 1]);
+      }
+      return half_swap_maximum(vmax(vmax(mc[0], mc[1]), vmax(sacc[0][15], sacc[1][15]))) * a.abs_scale_log2;
+    };
+    // S^T of one tile into sacc, masked on diagonal and ragged tiles
+    auto qk_tile = [&](int kb, int BUF, int SLOT, f32x16(&sacc)[2]) __attribute__((always_inline)) {
+  #pragma unroll
+      for (int s = 0; s < 2; ++s) {
+  #pragma unroll
+        for (int h = 0; h < KH; ++h) {
+          u32x4 kf[NDC / KH];
+          k_frags(BUF, SLOT, s, h, kf);
+          FE_PRIO_HI();
+  #pragma unroll
+          for (int c = 0; c < NDC / KH; ++c) {
+            const int cc = h * (NDC / KH) + c;
+            sacc[s] = cc == 0 ? E::mfma(kf[c], qf[0], (f32x16){}) : E::mfma(kf[c], qf[cc], sacc[s]);
           }
-        }
-  #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          float c4[4];
-  #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float e = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nb[i]));
-            if (i < 4)
-              c4[i] = e;
-            else
-              c4[i & 3] += e;
-          }
-          cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+          FE_PRIO_LO();
         }
       }
-      cs[0] = half_swap_sum(cs[0]);
-      cs[1] = half_swap_sum(cs[1]);
-      if (hh == 0) {
-        float* rb = red + BUF * NW * BN + wv * BN;
-        rb[l32] = cs[0];
-        rb[32 + l32] = cs[1];
+      if (kb + BN - 1 > lo_lim) {
+        // key kb + 32s + 8(i/4) + 4h + i%4 is visible iff its offset within the tile is at most
+        // rel: one subtraction per lane, then compares against inline constants
+        const int rel = qlim - kb - 4 * hh;
+  #pragma unroll
+        for (int s = 0; s < 2; ++s)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i)
+            sacc[s][i] = 32 * s + 8 * (i >> 2) + (i & 3) <= rel ? sacc[s][i] : NEG_INF;
+      }
+    };
+    // P = exp2(S*scale - m) packed to the input dtype, with per-lane partial sums of the
+    // rounded probabilities (pr). The EXACT flavour (replay rows) also returns the lane's FP32
+    // sum of the unrounded ones. The two flavours are separate code under a wave-uniform
+    // branch: folded into one, the compiler turns the condition into a select per element.
+    // S is consumed in place.
+    auto probs = [&](auto exact_tag, f32x16(&sacc)[2], u32x4(&pb)[4], float(&pr)[4]) __attribute__((always_inline)) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      float ps[4];
+  #pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float p[16];
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          p[i] = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nm));
+          if constexpr (EXACT) ps[i & 3] = s == 0 && i < 4 ? p[i] : ps[i & 3] + p[i];
+        }
+  #pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2)
+          pb[2 * s + c2] = (u32x4){E::pack2(p[8 * c2 + 0], p[8 * c2 + 1]), E::pack2(p[8 * c2 + 2], p[8 * c2 + 3]),
+                                   E::pack2(p[8 * c2 + 4], p[8 * c2 + 5]), E::pack2(p[8 * c2 + 6], p[8 * c2 + 7])};
+      }
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // zero-accumulator VOP3P form on the common path (see attn_rt2_kernel)
+        pr[j] = EXACT ? E::sum2(pb[0][j], ones2, 0.f) : E::sum2_0(pb[0][j], ones2);
+  #pragma unroll
+        for (int c = 1; c < 4; ++c) pr[j] = E::sum2(pb[c][j], ones2, pr[j]);
+      }
+      if constexpr (EXACT)
+        return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      else
+        return 0.f;
+    };
+    auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
+      const int kb = it * BN;
+      if (kb > wave_hi) return;
+
+      f32x16 sacc[2];
+      qk_tile(kb, BUF, SLOT, sacc);
+      if (fresh) {
+        // first tile of the row tile (O and the sums are still zero): exact max, no rescale
+        const float mt = exact_max(sacc);
+        m_run = mt;
+        nm = mt == NEG_INF ? 0.f : -mt;
+        fresh = false;
+      }
+      u32x4 pb[4];
+      float pr[4];
+      float le = probs(exact_tag, sacc, pb, pr);
+      // overflow guard on a lane's tile sum: the FP32 sum where it exists (ready right after the
+      // exponentials), else the rounded one
+      const float guard = decltype(exact_tag)::value ? le : (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      if (__any(guard > E::kMaxTileSum)) {
+        // S again (the tile is still in LDS), the new exact max, O and both sums rescaled,
+        // probabilities recomputed: now all at most 1
+        qk_tile(kb, BUF, SLOT, sacc);
+        const float mt = exact_max(sacc);
+        const float mn = vmax(m_run, mt);
+        const float corr = mn > m_run ? fast_exp2(m_run - mn) : 1.f;
+        l_run *= corr;
+        l_rnd *= corr;
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
+        m_run = mn;
+        nm = mn == NEG_INF ? 0.f : -mn;
+        le = probs(exact_tag, sacc, pb, pr);
+      }
+      l_rnd += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      if constexpr (decltype(exact_tag)::value) l_run += le;
+
+      if constexpr (NW > 8) {
+        // three waves per SIMD cover the V read latency; no prefetch (16 fewer registers)
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          u32x4 vf[4];
+  #pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) vf[c4] = v_frag(BUF, SLOT, c4, dt);
+          FE_PRIO_HI();
+  #pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[c4], pb[c4], o[dt]);
+          FE_PRIO_LO();
+        }
+      } else {
+        // V^T fragments of channel tile dt+1 are read while the MFMAs of tile dt run
+        u32x4 vf[2][4];
+  #pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) vf[0][c4] = v_frag(BUF, SLOT, c4, 0);
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          if (dt + 1 < NDT) {
+  #pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) vf[(dt + 1) & 1][c4] = v_frag(BUF, SLOT, c4, dt + 1);
+          }
+          FE_PRIO_HI();
+  #pragma unroll
+          for (int c4 = 0; c4 < 4; ++c4) o[dt] = E::mfma(vf[dt & 1][c4], pb[c4], o[dt]);
+          FE_PRIO_LO();
+        }
       }
     };
 
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // every wave is done reading the traversal-1 tiles
-    if (dmaw) dma_k(0, lds_k0);
-    for (int it = 0; it < ntiles; it += 2) {
-      t2_step(it, 0);
-      if (it + 1 < ntiles) t2_step(it + 1, 1);
+    if (dmaw) {
+  #pragma unroll
+      for (int sl = 0; sl < SLOTS; ++sl)
+        if (sl < ntiles) {
+          dma_k(sl * BN, lds_k0 + sl * TILE);
+          dma_v(sl * BN, lds_v0 + sl * TILE);
+        }
     }
-    __syncthreads();
-    flush((ntiles - 1) * BN, (ntiles - 1) & 1);
+    // The tile loop is instantiated twice, with and without the FP32 sum of the replay rows,
+    // and each wave runs one of them: the choice is made once per wave, not per tile.
+    auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
+      if constexpr (SLOTS == 2) {
+        for (int it = 0; it < ntiles; it += 4) {
+          t1_sync(it, 0);
+          t1_step(exact_tag, it, 0, 0);
+          if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
+          if (it + 2 < ntiles) {
+            t1_sync(it + 2, 1);
+            t1_step(exact_tag, it + 2, 1, 0);
+            if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+          }
+        }
+      } else {
+        for (int it = 0; it < ntiles; it += 2) {
+          t1_sync(it, 0);
+          t1_step(exact_tag, it, 0, 0);
+          if (it + 1 < ntiles) {
+            t1_sync(it + 1, 1);
+            t1_step(exact_tag, it + 1, 1, 0);
+          }
+        }
+      }
+    };
+    if (exact_l)
+      t1_loop(std::true_type{});
+    else
+      t1_loop(std::false_type{});
+
+    // ---------------- finish rows
+    const float l_tot = half_swap_sum(l_run);      // replay rows only
+    {
+      const int qi = q0 + l32;
+      if (tv && qi < N) {
+        const float inv = 1.f / half_swap_sum(l_rnd);
+        u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * (PARTIAL ? a.D : DP);
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+  #pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+            if (PARTIAL && d0 >= a.D) continue;    // channels past D (a multiple of 8) are not stored
+            const u32 w0 = E::pack2(o[dt][4 * g4 + 0] * inv, o[dt][4 * g4 + 1] * inv);
+            const u32 w1 = E::pack2(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv);
+            *(u32x2*)(op + d0) = (u32x2){w0, w1};
+          }
+        }
+      }
+    }
+
+    // ---------------- traversal 2: replay
+    if (!a.score) return;
+    if (a.bias) {
+      // Split schedule: hand the row's replay bias (see below) to replay_fast_kernel.
+      const int qi = q0 + l32;
+      if (hh == 0 && tv && qi < N) {
+        const bool live = qi >= a.win_lo;
+        a.bias[(long long)(b * a.Hq + head) * N + qi] =
+            live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+      }
+      return;
+    }
+    if constexpr (FUSED) {
+      if (wg_q_hi - 1 < a.win_lo) return;
+
+      // p_qk * w_q / l_q = exp2(s*scale - b_q) with b_q = m_q + log2 l_q - decay*log2e*(q-N+1),
+      // b_q = +inf for rows outside the window or past N. nb holds -b of the 16 rows of a lane.
+      float nb[16];
+      {
+        const int qi = q0 + l32;
+        const bool live = tv && qi < N && qi >= a.win_lo;
+        const float br = live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+    #pragma unroll
+        for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+      }
+      const bool rin = tv && q0 + 31 >= a.win_lo;
+      const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
+      float* imp_row = a.imp + (long long)bh * N;
+
+      // Flush of the previous tile's per-wave column sums (written before the barrier that
+      // precedes this call): one atomic per key per workgroup.
+      auto flush = [&](int kb_prev, int buf_prev) {
+        if (tid < BN) {
+          const float* rr = red + buf_prev * NW * BN + tid;
+          float sum = 0.f;
+    #pragma unroll
+          for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
+          const int key = kb_prev + tid;
+          if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+        }
+      };
+
+      // One 64-key tile: S = Q K^T (lanes hold keys), causal mask on diagonal tiles, column
+      // sums of exp2(S*scale - b_q) over this wave's 32 rows, written to LDS for the flush.
+      auto t2_step = [&](int it, int BUF) __attribute__((always_inline)) {
+        const int kb = it * BN;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (it > 0) flush(kb - BN, BUF ^ 1);
+        if (dmaw && it + 1 < ntiles) dma_k(kb + BN, BUF == 0 ? lds_k1 : lds_k0);
+        float cs[2] = {0.f, 0.f};
+        if (kb <= wave_hi_r) {
+          f32x16 sacc[2];
+    #pragma unroll
+          for (int s = 0; s < 2; ++s) {
+    #pragma unroll
+            for (int h = 0; h < KH; ++h) {
+              u32x4 kf[NDC / KH];
+              k_frags(BUF, 0, s, h, kf);
+              FE_PRIO_HI();
+    #pragma unroll
+              for (int c = 0; c < NDC / KH; ++c) {
+                const int cc = h * (NDC / KH) + c;
+                sacc[s] = cc == 0 ? E::mfma(qf[0], kf[c], (f32x16){}) : E::mfma(qf[cc], kf[c], sacc[s]);
+              }
+              FE_PRIO_LO();
+            }
+          }
+          if (a.causal && kb + BN - 1 > q0) {
+    #pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              // key kb + 32s + l32 against row q0 + 8(i/4) + 4h + i%4
+              const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+    #pragma unroll
+              for (int i = 0; i < 16; ++i) sacc[s][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[s][i];
+            }
+          }
+    #pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            float c4[4];
+    #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const float e = fast_exp2(fmaf(sacc[s][i], a.abs_scale_log2, nb[i]));
+              if (i < 4)
+                c4[i] = e;
+              else
+                c4[i & 3] += e;
+            }
+            cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+          }
+        }
+        cs[0] = half_swap_sum(cs[0]);
+        cs[1] = half_swap_sum(cs[1]);
+        if (hh == 0) {
+          float* rb = red + BUF * NW * BN + wv * BN;
+          rb[l32] = cs[0];
+          rb[32 + l32] = cs[1];
+        }
+      };
+
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // every wave is done reading the traversal-1 tiles
+      if (dmaw) dma_k(0, lds_k0);
+      for (int it = 0; it < ntiles; it += 2) {
+        t2_step(it, 0);
+        if (it + 1 < ntiles) t2_step(it + 1, 1);
+      }
+      __syncthreads();
+      flush((ntiles - 1) * BN, (ntiles - 1) & 1);
+    }
+  };
+  if constexpr (FUSED) {
+    // the kernel with the replay traversal (no workspace, so no queue) runs one item
+    run_item((int)blockIdx.x);
+  } else {
+    const int item_end = a.queue ? a.nitems : (int)blockIdx.x + 1;
+    for (int item = (int)blockIdx.x; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end)
+      run_item(item);
   }
 }
 
-// The lane's index, recomputed where it is used: opaque to the compiler, which would
-// otherwise keep values derived from it live across a tile loop and, at two or three
-// waves per SIMD, spill them (each reload then waits behind the next tile's DMA).
-__device__ __forceinline__ int lane_now() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
 
 // Traversal 1 (reference flash_evict/prefill.py:37-60) with two row tiles per wave (attention
 // only: the split schedule, or no importance), tile dims 96 and 128. Eight waves, two per SIMD, each holding the Q fragments
@@ -632,317 +731,326 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       lds_v0[SLOTS * TILE], lds_v1[SLOTS * TILE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
-  const int bh = (int)(blockIdx.x % (unsigned)a.BH);
-  const int wg = a.wg_bh - 1 - (int)(blockIdx.x / (unsigned)a.BH);
-  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
-  const int t_begin = wg * (NW * RT);
-  const int t_end = min(a.tiles_bh, t_begin + NW * RT);
-  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
-  const int kv_end = a.causal ? wg_q_hi : N;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  __shared__ int s_item;
+  int item = (int)blockIdx.x;
+  const int item_end = a.queue ? a.nitems : item + 1;
+  for (; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end) {
+    const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
+    // The divisors of the item decode, taken opaquely: otherwise the compiler keeps their
+    // reciprocals, computed once before the item loop, in registers across it.
+    int BH = a.BH, G = a.G, Hkv = a.Hkv;
+    asm volatile("" : "+s"(BH), "+s"(G), "+s"(Hkv));
+    const int bh = (int)((unsigned)item % (unsigned)BH);
+    const int wg = a.wg_bh - 1 - (int)((unsigned)item / (unsigned)BH);
+    const int b = bh / Hkv, hkv = bh - b * Hkv;
+    const int t_begin = wg * (NW * RT);
+    const int t_end = min(a.tiles_bh, t_begin + NW * RT);
+    const int wg_q_hi = min(N, ((t_end - 1) / G + 1) * 32);
+    const int kv_end = a.causal ? wg_q_hi : N;
+    const int ntiles = (kv_end + BN - 1) / BN;
 
-  // This wave's row tiles j = 0, 1: 32 query positions from q0[j] of query head head[j].
-  // lo_lim: below it no key of either tile is masked; wave_hi: past it every key of both tiles
-  // is.
-  int q0[RT], head[RT];
-  bool tv[RT];
-  int lo_lim = N, wave_hi = -1;
-  bool in_win = false;
-#pragma unroll
-  for (int j = 0; j < RT; ++j) {
-    const int t = t_begin + RT * wv + j;
-    tv[j] = t < t_end;
-    const int tt = tv[j] ? t : t_begin;
-    q0[j] = (tt / a.G) * 32;
-    head[j] = hkv * a.G + (tt - (tt / a.G) * a.G);
-    lo_lim = min(lo_lim, !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1));
-    wave_hi = max(wave_hi, !tv[j] ? -1 : (a.causal ? min(q0[j] + 31, N - 1) : N - 1));
-    in_win = in_win || (tv[j] && q0[j] + 31 >= a.win_lo);
-  }
-
-  const u32 qneg = a.neg_scale ? 0x80008000u : 0u;   // a negative scale runs as |scale| on -Q
-  u32x4 qf[RT][NDC];
-#pragma unroll
-  for (int j = 0; j < RT; ++j) {
-    const int qr = q0[j] + l32;
-    const bool ok = tv[j] && qr < N;
-    const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
-#pragma unroll
-    for (int c = 0; c < NDC; ++c)
-      qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
-  }
-
-  // LDS operand offsets and tile DMA: the layout of fused_fast_kernel
-  const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
-  u32 voff;
-  {
-    const int r = lane & 15, g = lane >> 4;
-    voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
-  }
-  const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
-  const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
-  const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
-  // per-lane DMA offsets (see fused_fast_kernel), recomputed at each DMA: held across the
-  // tile loop they would take registers the two row tiles need
-  auto dma_k = [&](int kb, unsigned char* ldst) {
-    const int ln = lane_now();
-    const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
-    dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
-  };
-  auto dma_v = [&](int kb, unsigned char* ldst) {
-    const int ln = lane_now();
-    dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, (u32)(ln >> 2) * vrow + (u32)((ln & 3) << 4), kb, N, ldst, wv, a.D,
-                                  (u32)((ln & 3) << 3));
-  };
-
-  // K fragments c0 .. c0+KG-1 of keys 32s + l32 (buffer BUF, slot SLOT)
-  auto k_frags = [&](int BUF, int SLOT, int s, int c0, u32x4(&kf)[KG]) __attribute__((always_inline)) {
-    const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
-#pragma unroll
-    for (int c = 0; c < KG; ++c) kf[c] = *(const u32x4*)(kt + (c0 + c) * 2048);
-  };
-  auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
-    const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
-    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
-    const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
-    const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
-    return (u32x4){ux[0], ux[1], uy[0], uy[1]};
-  };
-
-  f32x16 o[RT][NDT];
-  // nm: minus the row's reference max (log2 units); 0 while a padding tile has seen no key
-  float l_run[RT], l_rnd[RT], nm[RT];
-#pragma unroll
-  for (int j = 0; j < RT; ++j) {
-    l_run[j] = 0.f;
-    l_rnd[j] = 0.f;
-    nm[j] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = (f32x16){};
-  }
-  bool fresh = true;                             // no key of this wave's tiles seen yet
-  // Only rows the replay visits need the FP32 sum (their replay bias); wave-uniform.
-  const bool exact_l = a.score && in_win;
-  u32 ones2;
-  asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
-
-  auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (dmaw) {
-#pragma unroll
-      for (int sl = 0; sl < SLOTS; ++sl)
-        if (it + SLOTS + sl < ntiles) {
-          dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
-          dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
-        }
-    }
-  };
-  // Key kh + 8(i/4) + 4h + i%4 (accumulator register i) is visible to the lane's query row of
-  // tile j iff 8(i/4) + i%4 <= mask_rel(j, kh): the row's last visible key (-1 for a padding
-  // tile) minus kh + 4h. Lane-derived, so recomputed here (diagonal and ragged halves only).
-  auto mask_rel = [&](int j, int kh) __attribute__((always_inline)) -> int {
-    const int ln = lane_now();
-    const int ql = !tv[j] ? -1 : (a.causal ? min(q0[j] + (ln & 31), N - 1) : N - 1);
-    return ql - kh - 4 * (ln >> 5);
-  };
-  // S^T of keys kh .. kh+31 for both row tiles (lanes hold queries; register i holds key
-  // kh + 8(i/4) + 4h + i%4), masked on diagonal and ragged halves
-  auto qk_half = [&](int kh, int BUF, int SLOT, int s, f32x16(&S)[RT]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int g = 0; g < NDC / KG; ++g) {
-      u32x4 kf[KG];
-      k_frags(BUF, SLOT, s, g * KG, kf);
-      FE_PRIO_HI();
-#pragma unroll
-      for (int c = 0; c < KG; ++c)
-#pragma unroll
-        for (int j = 0; j < RT; ++j)
-          S[j] = (g == 0 && c == 0) ? E::mfma(kf[0], qf[j][0], (f32x16){}) : E::mfma(kf[c], qf[j][g * KG + c], S[j]);
-      FE_PRIO_LO();
-    }
-    if (kh + 31 > lo_lim) {
-#pragma unroll
-      for (int j = 0; j < RT; ++j) {
-        const int rel = mask_rel(j, kh);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S[j][i] = 8 * (i >> 2) + (i & 3) <= rel ? S[j][i] : NEG_INF;
-      }
-    }
-  };
-  // the same for row tile J alone (the rare overflow recompute)
-  auto qk_one = [&](auto jtag, int kh, int BUF, int SLOT, int s, f32x16& S) __attribute__((always_inline)) {
-    constexpr int J = decltype(jtag)::value;
-#pragma unroll
-    for (int g = 0; g < NDC / KG; ++g) {
-      u32x4 kf[KG];
-      k_frags(BUF, SLOT, s, g * KG, kf);
-#pragma unroll
-      for (int c = 0; c < KG; ++c) S = (g == 0 && c == 0) ? E::mfma(kf[0], qf[J][0], (f32x16){}) : E::mfma(kf[c], qf[J][g * KG + c], S);
-    }
-    if (kh + 31 > lo_lim) {
-      const int rel = mask_rel(J, kh);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) S[i] = 8 * (i >> 2) + (i & 3) <= rel ? S[i] : NEG_INF;
-    }
-  };
-  // exact max (log2 units) of a row over the 32 keys of S: this lane's 16 and the other half-wave's
-  auto exact_max = [&](const f32x16& S) __attribute__((always_inline)) -> float {
-    float mc = vmax(vmax(S[0], S[1]), S[2]);
-#pragma unroll
-    for (int i = 3; i < 15; i += 2) mc = vmax(vmax(mc, S[i]), S[i + 1]);
-    return half_swap_maximum(vmax(mc, S[15])) * a.abs_scale_log2;
-  };
-  // P = exp2(S*scale - m) packed to the input dtype (pb[0]: keys 0-15 of the half, pb[1]:
-  // 16-31), partial sums of the rounded probabilities (pr); EXACT also returns the lane's
-  // FP32 sum of the unrounded ones
-  // S is consumed in place (it holds the probabilities afterwards).
-  auto probs = [&](auto exact_tag, f32x16& S, float nmj, u32x4(&pb)[2], float(&pr)[4]) __attribute__((always_inline)) {
-    constexpr bool EXACT = decltype(exact_tag)::value;
-    float ps[4];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      S[i] = fast_exp2(fmaf(S[i], a.abs_scale_log2, nmj));
-      if constexpr (EXACT) ps[i & 3] = i < 4 ? S[i] : ps[i & 3] + S[i];
-    }
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-      pb[c2] = (u32x4){E::pack2(S[8 * c2 + 0], S[8 * c2 + 1]), E::pack2(S[8 * c2 + 2], S[8 * c2 + 3]),
-                       E::pack2(S[8 * c2 + 4], S[8 * c2 + 5]), E::pack2(S[8 * c2 + 6], S[8 * c2 + 7])};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // the zero-accumulator VOP3P form saves a v_mov per chain; measured 1-2% faster on the
-      // common path, 1.5% slower in the replay-row variant (the compiler schedules it worse)
-      const float first = EXACT ? E::sum2(pb[0][e], ones2, 0.f) : E::sum2_0(pb[0][e], ones2);
-      pr[e] = E::sum2(pb[1][e], ones2, first);
-    }
-    if constexpr (EXACT)
-      return (ps[0] + ps[1]) + (ps[2] + ps[3]);
-    else
-      return 0.f;
-  };
-  // overflow path of row tile J: S again, the new exact max, O and both sums rescaled,
-  // probabilities recomputed (now at most 1)
-  auto rescale_one = [&](auto exact_tag, auto jtag, int kh, int BUF, int SLOT, int s, u32x4(&pb)[2], float(&pr)[4])
-                         __attribute__((always_inline)) -> float {
-    constexpr int J = decltype(jtag)::value;
-    f32x16 S;
-    qk_one(jtag, kh, BUF, SLOT, s, S);
-    // a row that overflows has a finite reference max (its tile is a real one)
-    const float m_old = -nm[J];
-    const float mn = vmax(m_old, exact_max(S));
-    const float corr = mn > m_old ? fast_exp2(m_old - mn) : 1.f;
-    l_run[J] *= corr;
-    l_rnd[J] *= corr;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[J][dt] *= corr;
-    nm[J] = -mn;
-    return probs(exact_tag, S, nm[J], pb, pr);
-  };
-  // keys 32s .. 32s+31 of tile it (buffer BUF, slot SLOT)
-  auto t1_half = [&](auto exact_tag, int it, int BUF, int SLOT, int s) __attribute__((always_inline)) {
-    constexpr bool EXACT = decltype(exact_tag)::value;
-    const int kh = it * BN + 32 * s;
-    if (kh > wave_hi) return;
-
-    f32x16 S[RT];
-    qk_half(kh, BUF, SLOT, s, S);
-    if (fresh) {
-      // first keys of the row tiles (O and the sums are still zero): exact max, no rescale
-#pragma unroll
-      for (int j = 0; j < RT; ++j) {
-        const float mt = exact_max(S[j]);
-        nm[j] = mt == NEG_INF ? 0.f : -mt;
-      }
-      fresh = false;
-    }
-    u32x4 pb[RT][2];
-    float pr[RT][4], le[RT];
-#pragma unroll
-    for (int j = 0; j < RT; ++j) le[j] = probs(exact_tag, S[j], nm[j], pb[j], pr[j]);
-    {
-      const float g0 = EXACT ? le[0] : (pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3]);
-      if (__any(g0 > E::kMaxTileSum)) le[0] = rescale_one(exact_tag, std::integral_constant<int, 0>{}, kh, BUF, SLOT, s, pb[0], pr[0]);
-      const float g1 = EXACT ? le[1] : (pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]);
-      if (__any(g1 > E::kMaxTileSum)) le[1] = rescale_one(exact_tag, std::integral_constant<int, 1>{}, kh, BUF, SLOT, s, pb[1], pr[1]);
-    }
-#pragma unroll
+    // This wave's row tiles j = 0, 1: 32 query positions from q0[j] of query head head[j].
+    // lo_lim: below it no key of either tile is masked; wave_hi: past it every key of both tiles
+    // is.
+    int q0[RT], head[RT];
+    bool tv[RT];
+    int lo_lim = N, wave_hi = -1;
+    bool in_win = false;
+  #pragma unroll
     for (int j = 0; j < RT; ++j) {
-      l_rnd[j] += (pr[j][0] + pr[j][1]) + (pr[j][2] + pr[j][3]);
-      if constexpr (EXACT) l_run[j] += le[j];
+      const int t = t_begin + RT * wv + j;
+      tv[j] = t < t_end;
+      const int tt = tv[j] ? t : t_begin;
+      q0[j] = (tt / G) * 32;
+      head[j] = hkv * G + (tt - (tt / G) * G);
+      lo_lim = min(lo_lim, !tv[j] ? -1 : (a.causal ? min(q0[j], N - 1) : N - 1));
+      wave_hi = max(wave_hi, !tv[j] ? -1 : (a.causal ? min(q0[j] + 31, N - 1) : N - 1));
+      in_win = in_win || (tv[j] && q0[j] + 31 >= a.win_lo);
     }
-    // O^T += V^T P^T over the half's two 16-key groups; each V^T fragment feeds both row tiles
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      u32x4 vf[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) vf[c] = v_frag(BUF, SLOT, 2 * s + c, dt);
-      FE_PRIO_HI();
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int j = 0; j < RT; ++j) o[j][dt] = E::mfma(vf[c], pb[j][c], o[j][dt]);
-      FE_PRIO_LO();
-    }
-  };
-  auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
-    t1_half(exact_tag, it, BUF, SLOT, 0);
-    t1_half(exact_tag, it, BUF, SLOT, 1);
-  };
 
-  if (dmaw) {
-#pragma unroll
-    for (int sl = 0; sl < SLOTS; ++sl)
-      if (sl < ntiles) {
-        dma_k(sl * BN, lds_k0 + sl * TILE);
-        dma_v(sl * BN, lds_v0 + sl * TILE);
-      }
-  }
-  auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
-    for (int it = 0; it < ntiles; it += 4) {
-      t1_sync(it, 0);
-      t1_step(exact_tag, it, 0, 0);
-      if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
-      if (it + 2 < ntiles) {
-        t1_sync(it + 2, 1);
-        t1_step(exact_tag, it + 2, 1, 0);
-        if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
-      }
+    const u32 qneg = a.neg_scale ? 0x80008000u : 0u;   // a negative scale runs as |scale| on -Q
+    u32x4 qf[RT][NDC];
+  #pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int qr = q0[j] + l32;
+      const bool ok = tv[j] && qr < N;
+      const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+  #pragma unroll
+      for (int c = 0; c < NDC; ++c)
+        qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     }
-  };
-  if (exact_l)
-    t1_loop(std::true_type{});
-  else
-    t1_loop(std::false_type{});
 
-  // ---------------- finish rows: O / l_rnd, and the replay bias
-#pragma unroll
-  for (int j = 0; j < RT; ++j) {
-    const float l_tot = half_swap_sum(l_run[j]);
-    const float inv = 1.f / half_swap_sum(l_rnd[j]);
-    const int qi = q0[j] + l32;
-    if (tv[j] && qi < N) {
-      u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * (PARTIAL ? a.D : DP);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d0 = 32 * dt + 8 * g4 + 4 * hh;
-          if (PARTIAL && d0 >= a.D) continue;
-          const u32 w0 = E::pack2(o[j][dt][4 * g4 + 0] * inv, o[j][dt][4 * g4 + 1] * inv);
-          const u32 w1 = E::pack2(o[j][dt][4 * g4 + 2] * inv, o[j][dt][4 * g4 + 3] * inv);
-          *(u32x2*)(op + d0) = (u32x2){w0, w1};
+    // LDS operand offsets and tile DMA: the layout of fused_fast_kernel
+    const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+    u32 voff;
+    {
+      const int r = lane & 15, g = lane >> 4;
+      voff = (u32)((4 * hh + (r >> 2)) * 64 + 32 * (g & 1) + 8 * (r & 3));
+    }
+    const u32 krow = (u32)(a.ks[2] * 2), vrow = (u32)(a.vs[2] * 2);
+    const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+    const unsigned char* vg = (const unsigned char*)(a.v + b * a.vs[0] + hkv * a.vs[1]);
+    // per-lane DMA offsets (see fused_fast_kernel), recomputed at each DMA: held across the
+    // tile loop they would take registers the two row tiles need
+    auto dma_k = [&](int kb, unsigned char* ldst) {
+      const int ln = lane_now();
+      const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
+      dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
+    };
+    auto dma_v = [&](int kb, unsigned char* ldst) {
+      const int ln = lane_now();
+      dma_tile_cm<DPW, 64, PARTIAL>(vg, vrow, (u32)(ln >> 2) * vrow + (u32)((ln & 3) << 4), kb, N, ldst, wv, a.D,
+                                    (u32)((ln & 3) << 3));
+    };
+
+    // K fragments c0 .. c0+KG-1 of keys 32s + l32 (buffer BUF, slot SLOT)
+    auto k_frags = [&](int BUF, int SLOT, int s, int c0, u32x4(&kf)[KG]) __attribute__((always_inline)) {
+      const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE + s * 1024 + koff;
+  #pragma unroll
+      for (int c = 0; c < KG; ++c) kf[c] = *(const u32x4*)(kt + (c0 + c) * 2048);
+    };
+    auto v_frag = [&](int BUF, int SLOT, int c4, int dt) __attribute__((always_inline)) -> u32x4 {
+      const unsigned char* vt = (BUF == 0 ? lds_v0 : lds_v1) + SLOT * TILE + dt * 4096 + c4 * 1024 + voff;
+      const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)vt);
+      const s16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr_t)(vt + 512));
+      const u32x2 ux = __builtin_bit_cast(u32x2, x), uy = __builtin_bit_cast(u32x2, y);
+      return (u32x4){ux[0], ux[1], uy[0], uy[1]};
+    };
+
+    f32x16 o[RT][NDT];
+    // nm: minus the row's reference max (log2 units); 0 while a padding tile has seen no key
+    float l_run[RT], l_rnd[RT], nm[RT];
+  #pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      l_run[j] = 0.f;
+      l_rnd[j] = 0.f;
+      nm[j] = 0.f;
+  #pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[j][dt] = (f32x16){};
+    }
+    bool fresh = true;                             // no key of this wave's tiles seen yet
+    // Only rows the replay visits need the FP32 sum (their replay bias); wave-uniform.
+    const bool exact_l = a.score && in_win;
+    u32 ones2;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(ones2) : "i"(E::kOnes2));
+
+    auto t1_sync = [&](int it, int BUF) __attribute__((always_inline)) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (dmaw) {
+  #pragma unroll
+        for (int sl = 0; sl < SLOTS; ++sl)
+          if (it + SLOTS + sl < ntiles) {
+            dma_k((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+            dma_v((it + SLOTS + sl) * BN, (BUF == 0 ? lds_v1 : lds_v0) + sl * TILE);
+          }
+      }
+    };
+    // Key kh + 8(i/4) + 4h + i%4 (accumulator register i) is visible to the lane's query row of
+    // tile j iff 8(i/4) + i%4 <= mask_rel(j, kh): the row's last visible key (-1 for a padding
+    // tile) minus kh + 4h. Lane-derived, so recomputed here (diagonal and ragged halves only).
+    auto mask_rel = [&](int j, int kh) __attribute__((always_inline)) -> int {
+      const int ln = lane_now();
+      const int ql = !tv[j] ? -1 : (a.causal ? min(q0[j] + (ln & 31), N - 1) : N - 1);
+      return ql - kh - 4 * (ln >> 5);
+    };
+    // S^T of keys kh .. kh+31 for both row tiles (lanes hold queries; register i holds key
+    // kh + 8(i/4) + 4h + i%4), masked on diagonal and ragged halves
+    auto qk_half = [&](int kh, int BUF, int SLOT, int s, f32x16(&S)[RT]) __attribute__((always_inline)) {
+  #pragma unroll
+      for (int g = 0; g < NDC / KG; ++g) {
+        u32x4 kf[KG];
+        k_frags(BUF, SLOT, s, g * KG, kf);
+        FE_PRIO_HI();
+  #pragma unroll
+        for (int c = 0; c < KG; ++c)
+  #pragma unroll
+          for (int j = 0; j < RT; ++j)
+            S[j] = (g == 0 && c == 0) ? E::mfma(kf[0], qf[j][0], (f32x16){}) : E::mfma(kf[c], qf[j][g * KG + c], S[j]);
+        FE_PRIO_LO();
+      }
+      if (kh + 31 > lo_lim) {
+  #pragma unroll
+        for (int j = 0; j < RT; ++j) {
+          const int rel = mask_rel(j, kh);
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) S[j][i] = 8 * (i >> 2) + (i & 3) <= rel ? S[j][i] : NEG_INF;
         }
       }
-      if (a.score && a.bias && hh == 0) {
-        const bool live = qi >= a.win_lo;
-        a.bias[(long long)(b * a.Hq + head[j]) * N + qi] =
-            live ? (fast_log2(l_tot) - nm[j] - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+    };
+    // the same for row tile J alone (the rare overflow recompute)
+    auto qk_one = [&](auto jtag, int kh, int BUF, int SLOT, int s, f32x16& S) __attribute__((always_inline)) {
+      constexpr int J = decltype(jtag)::value;
+  #pragma unroll
+      for (int g = 0; g < NDC / KG; ++g) {
+        u32x4 kf[KG];
+        k_frags(BUF, SLOT, s, g * KG, kf);
+  #pragma unroll
+        for (int c = 0; c < KG; ++c) S = (g == 0 && c == 0) ? E::mfma(kf[0], qf[J][0], (f32x16){}) : E::mfma(kf[c], qf[J][g * KG + c], S);
+      }
+      if (kh + 31 > lo_lim) {
+        const int rel = mask_rel(J, kh);
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = 8 * (i >> 2) + (i & 3) <= rel ? S[i] : NEG_INF;
+      }
+    };
+    // exact max (log2 units) of a row over the 32 keys of S: this lane's 16 and the other half-wave's
+    auto exact_max = [&](const f32x16& S) __attribute__((always_inline)) -> float {
+      float mc = vmax(vmax(S[0], S[1]), S[2]);
+  #pragma unroll
+      for (int i = 3; i < 15; i += 2) mc = vmax(vmax(mc, S[i]), S[i + 1]);
+      return half_swap_maximum(vmax(mc, S[15])) * a.abs_scale_log2;
+    };
+    // P = exp2(S*scale - m) packed to the input dtype (pb[0]: keys 0-15 of the half, pb[1]:
+    // 16-31), partial sums of the rounded probabilities (pr); EXACT also returns the lane's
+    // FP32 sum of the unrounded ones
+    // S is consumed in place (it holds the probabilities afterwards).
+    auto probs = [&](auto exact_tag, f32x16& S, float nmj, u32x4(&pb)[2], float(&pr)[4]) __attribute__((always_inline)) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      float ps[4];
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        S[i] = fast_exp2(fmaf(S[i], a.abs_scale_log2, nmj));
+        if constexpr (EXACT) ps[i & 3] = i < 4 ? S[i] : ps[i & 3] + S[i];
+      }
+  #pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2)
+        pb[c2] = (u32x4){E::pack2(S[8 * c2 + 0], S[8 * c2 + 1]), E::pack2(S[8 * c2 + 2], S[8 * c2 + 3]),
+                         E::pack2(S[8 * c2 + 4], S[8 * c2 + 5]), E::pack2(S[8 * c2 + 6], S[8 * c2 + 7])};
+  #pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // the zero-accumulator VOP3P form saves a v_mov per chain; measured 1-2% faster on the
+        // common path, 1.5% slower in the replay-row variant (the compiler schedules it worse)
+        const float first = EXACT ? E::sum2(pb[0][e], ones2, 0.f) : E::sum2_0(pb[0][e], ones2);
+        pr[e] = E::sum2(pb[1][e], ones2, first);
+      }
+      if constexpr (EXACT)
+        return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      else
+        return 0.f;
+    };
+    // overflow path of row tile J: S again, the new exact max, O and both sums rescaled,
+    // probabilities recomputed (now at most 1)
+    auto rescale_one = [&](auto exact_tag, auto jtag, int kh, int BUF, int SLOT, int s, u32x4(&pb)[2], float(&pr)[4])
+                           __attribute__((always_inline)) -> float {
+      constexpr int J = decltype(jtag)::value;
+      f32x16 S;
+      qk_one(jtag, kh, BUF, SLOT, s, S);
+      // a row that overflows has a finite reference max (its tile is a real one)
+      const float m_old = -nm[J];
+      const float mn = vmax(m_old, exact_max(S));
+      const float corr = mn > m_old ? fast_exp2(m_old - mn) : 1.f;
+      l_run[J] *= corr;
+      l_rnd[J] *= corr;
+  #pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[J][dt] *= corr;
+      nm[J] = -mn;
+      return probs(exact_tag, S, nm[J], pb, pr);
+    };
+    // keys 32s .. 32s+31 of tile it (buffer BUF, slot SLOT)
+    auto t1_half = [&](auto exact_tag, int it, int BUF, int SLOT, int s) __attribute__((always_inline)) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      const int kh = it * BN + 32 * s;
+      if (kh > wave_hi) return;
+
+      f32x16 S[RT];
+      qk_half(kh, BUF, SLOT, s, S);
+      if (fresh) {
+        // first keys of the row tiles (O and the sums are still zero): exact max, no rescale
+  #pragma unroll
+        for (int j = 0; j < RT; ++j) {
+          const float mt = exact_max(S[j]);
+          nm[j] = mt == NEG_INF ? 0.f : -mt;
+        }
+        fresh = false;
+      }
+      u32x4 pb[RT][2];
+      float pr[RT][4], le[RT];
+  #pragma unroll
+      for (int j = 0; j < RT; ++j) le[j] = probs(exact_tag, S[j], nm[j], pb[j], pr[j]);
+      {
+        const float g0 = EXACT ? le[0] : (pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3]);
+        if (__any(g0 > E::kMaxTileSum)) le[0] = rescale_one(exact_tag, std::integral_constant<int, 0>{}, kh, BUF, SLOT, s, pb[0], pr[0]);
+        const float g1 = EXACT ? le[1] : (pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]);
+        if (__any(g1 > E::kMaxTileSum)) le[1] = rescale_one(exact_tag, std::integral_constant<int, 1>{}, kh, BUF, SLOT, s, pb[1], pr[1]);
+      }
+  #pragma unroll
+      for (int j = 0; j < RT; ++j) {
+        l_rnd[j] += (pr[j][0] + pr[j][1]) + (pr[j][2] + pr[j][3]);
+        if constexpr (EXACT) l_run[j] += le[j];
+      }
+      // O^T += V^T P^T over the half's two 16-key groups; each V^T fragment feeds both row tiles
+  #pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        u32x4 vf[2];
+  #pragma unroll
+        for (int c = 0; c < 2; ++c) vf[c] = v_frag(BUF, SLOT, 2 * s + c, dt);
+        FE_PRIO_HI();
+  #pragma unroll
+        for (int c = 0; c < 2; ++c)
+  #pragma unroll
+          for (int j = 0; j < RT; ++j) o[j][dt] = E::mfma(vf[c], pb[j][c], o[j][dt]);
+        FE_PRIO_LO();
+      }
+    };
+    auto t1_step = [&](auto exact_tag, int it, int BUF, int SLOT) __attribute__((always_inline)) {
+      t1_half(exact_tag, it, BUF, SLOT, 0);
+      t1_half(exact_tag, it, BUF, SLOT, 1);
+    };
+
+    if (dmaw) {
+  #pragma unroll
+      for (int sl = 0; sl < SLOTS; ++sl)
+        if (sl < ntiles) {
+          dma_k(sl * BN, lds_k0 + sl * TILE);
+          dma_v(sl * BN, lds_v0 + sl * TILE);
+        }
+    }
+    auto t1_loop = [&](auto exact_tag) __attribute__((always_inline)) {
+      for (int it = 0; it < ntiles; it += 4) {
+        t1_sync(it, 0);
+        t1_step(exact_tag, it, 0, 0);
+        if (it + 1 < ntiles) t1_step(exact_tag, it + 1, 0, 1);
+        if (it + 2 < ntiles) {
+          t1_sync(it + 2, 1);
+          t1_step(exact_tag, it + 2, 1, 0);
+          if (it + 3 < ntiles) t1_step(exact_tag, it + 3, 1, 1);
+        }
+      }
+    };
+    if (exact_l)
+      t1_loop(std::true_type{});
+    else
+      t1_loop(std::false_type{});
+
+    // ---------------- finish rows: O / l_rnd, and the replay bias
+  #pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const float l_tot = half_swap_sum(l_run[j]);
+      const float inv = 1.f / half_swap_sum(l_rnd[j]);
+      const int qi = q0[j] + l32;
+      if (tv[j] && qi < N) {
+        u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * (PARTIAL ? a.D : DP);
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+  #pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+            if (PARTIAL && d0 >= a.D) continue;
+            const u32 w0 = E::pack2(o[j][dt][4 * g4 + 0] * inv, o[j][dt][4 * g4 + 1] * inv);
+            const u32 w1 = E::pack2(o[j][dt][4 * g4 + 2] * inv, o[j][dt][4 * g4 + 3] * inv);
+            *(u32x2*)(op + d0) = (u32x2){w0, w1};
+          }
+        }
+        if (a.score && a.bias && hh == 0) {
+          const bool live = qi >= a.win_lo;
+          a.bias[(long long)(b * a.Hq + head[j]) * N + qi] =
+              live ? (fast_log2(l_tot) - nm[j] - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+        }
       }
     }
   }
@@ -987,7 +1095,6 @@ __global__ __launch_bounds__((64 * ReplayShape<TPW, DP>::NW), (ReplayShape<TPW, 
   __shared__ float red[2 * NW * BN];              // [2][NW][BN] per-wave column sums
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
@@ -995,17 +1102,22 @@ __global__ __launch_bounds__((64 * ReplayShape<TPW, DP>::NW), (ReplayShape<TPW, 
   // Heaviest causal query blocks first; the grid covers only workgroups with window rows.
   // With few such workgroups (a short observation window) each one's keys are split over
   // a.rsplit blocks (block-uniform: an empty share exits before any barrier).
-  const int ks = (int)(blockIdx.x % (unsigned)a.rsplit);
-  const int rest = (int)(blockIdx.x / (unsigned)a.rsplit);
-  const int bh = rest % a.BH;
-  const int wg = a.wg_bh - 1 - rest / a.BH;
-  const int b = bh / a.Hkv, hkv = bh - b * a.Hkv;
+  __shared__ int s_item;
+  const int item = block_item(a, &s_item, wv);
+  if (item >= (a.queue ? a.nitems : (int)gridDim.x)) return;
+  const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
+  const int BH = a.BH, G = a.G, Hkv = a.Hkv, rsplit = a.rsplit;
+  const int bh = (int)((unsigned)item % (unsigned)BH);
+  const int rest = (int)((unsigned)item / (unsigned)BH);
+  const int ks = rest % rsplit;
+  const int wg = a.wg_bh - 1 - rest / rsplit;
+  const int b = bh / Hkv, hkv = bh - b * Hkv;
   const int t_begin = wg * RT;
   const int t_end = min(a.tiles_bh, t_begin + RT);
-  const int wg_q_hi = min(N, ((t_end - 1) / a.G + 1) * 32);
+  const int wg_q_hi = min(N, ((t_end - 1) / G + 1) * 32);
   const int kv_end = a.causal ? wg_q_hi : N;
   const int ntiles_all = (kv_end + BN - 1) / BN;
-  const int per = (ntiles_all + a.rsplit - 1) / a.rsplit;
+  const int per = (ntiles_all + rsplit - 1) / rsplit;
   const int it_lo = ks * per;                     // this block's key tiles [it_lo, ntiles)
   const int ntiles = min(ntiles_all, it_lo + per);
   if (it_lo >= ntiles) return;
@@ -1023,8 +1135,8 @@ __global__ __launch_bounds__((64 * ReplayShape<TPW, DP>::NW), (ReplayShape<TPW, 
     const int t = t_begin + TPW * wv + j;
     const bool tv = t < t_end;
     const int tt = tv ? t : t_begin;
-    q0[j] = (tt / a.G) * 32;
-    const int head = hkv * a.G + (tt - (tt / a.G) * a.G);
+    q0[j] = (tt / G) * 32;
+    const int head = hkv * G + (tt - (tt / G) * G);
     const bool rin = tv && q0[j] + 31 >= a.win_lo;
     if (rin) wave_hi = max(wave_hi, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
     const int qr = q0[j] + l32;

@@ -81,18 +81,25 @@ int fe_prefill(const void* q, const void* k, const void* v, void* out, float* im
 int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
 
 /*
- * fe_prefill with a caller-provided workspace (same contract). With at least
- * fe_prefill_workspace_bytes() bytes (B*Hq*N floats when
- * score != 0, else 0) and the fast layouts (D a multiple of 8 up to 256, nonzero scale, unit-stride
- * 16-byte aligned K/V rows; Q of any strides),
- * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
- * per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace. At head dims
- * 72..128 (multiples of 8) its attention kernel holds two row tiles per wave and takes a row's
- * reference max over its first 32 keys instead of 64: the output then agrees with fe_prefill's
- * to within two roundings of the probabilities, the importance to FP32 summation order; at
- * other head dims the output is bitwise equal and the importance equal up to FP32 atomic
- * order. With less workspace (or NULL) this is fe_prefill. Same reference interface as
- * fe_prefill.
+ * fe_prefill with a caller-provided workspace (same contract). fe_prefill_workspace_bytes()
+ * is B*Hq*N floats of replay biases (score != 0; none otherwise), rounded up to 256 bytes,
+ * plus 2 KiB of work-item counters. With the fast layouts (D a multiple of 8 up to 256,
+ * nonzero scale, unit-stride 16-byte aligned K/V rows; Q of any strides):
+ *   * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
+ *     per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace;
+ *   * with the whole workspace, the work items of the attention and replay kernels (groups of
+ *     query rows, heaviest first) are taken from per-XCD queues in the counters as CUs free
+ *     up (the call zeroes them first), instead of one per workgroup index. Each item is
+ *     computed the same way whichever workgroup takes it: the output is bitwise that of the
+ *     static schedule, the importance equal up to FP32 atomic order;
+ *   * score == 0 uses the counters alone.
+ * At head dims 72..128 (multiples of 8) the split schedule's attention kernel holds two row
+ * tiles per wave and takes a row's reference max over its first 32 keys instead of 64: the
+ * output then agrees with fe_prefill's to within two roundings of the probabilities, the
+ * importance to FP32 summation order; at other head dims the output is bitwise equal and the
+ * importance equal up to FP32 atomic order. With room for the biases but not the counters
+ * the schedule is static; with less workspace (or NULL) this is fe_prefill. Same reference
+ * interface as fe_prefill.
  */
 size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score);
 int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance,
@@ -108,12 +115,12 @@ int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float*
  * routine (and no timing events: fe_fused_timing_enable does not apply to it). No
  * counterpart in the reference; it is for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The buffer holds FE_STATIC_BIAS_ROWS floats (16 MiB) on every GPU the library runs on,
- * kept until the process ends. A scoring call needs B*Hq*N <= FE_STATIC_BIAS_ROWS and
- * otherwise fails with FE_ERR_WORKSPACE before launching anything. Every call on one GPU
- * shares that GPU's buffer: calls that overlap on one GPU (concurrent streams or threads)
- * race, so the caller must order them. Results: those of fe_prefill_ws (bitwise output,
- * importance up to FP32 atomic order).
+ * The buffer holds FE_STATIC_BIAS_ROWS floats and the work-item counters (16 MiB + 2 KiB) on
+ * every GPU the library runs on, kept until the process ends. A scoring call needs
+ * B*Hq*N <= FE_STATIC_BIAS_ROWS and otherwise fails with FE_ERR_WORKSPACE before launching
+ * anything. Every call on one GPU shares that GPU's buffer: calls that overlap on one GPU
+ * (concurrent streams or threads) race, so the caller must order them. Results: those of
+ * fe_prefill_ws with its whole workspace (bitwise output, importance up to FP32 atomic order).
  */
 #define FE_STATIC_BIAS_ROWS 4194304
 int fe_prefill_static(const void* q, const void* k, const void* v, void* out, float* importance,

@@ -20,7 +20,15 @@ from _helpers import assert_schedules_agree, seeded_randn, split_runs_two_row_ti
 pytestmark = pytest.mark.gpu
 
 
-def _run(q, k, v, causal, weighted, decay, window, use_ws):
+def _ws_layout(b, h, n, score):
+    """fe_prefill_workspace_bytes: B*Hq*N floats of replay biases (scoring calls), then 2 KiB
+    of work-item counters for the dynamic schedule (eight queues per kernel, one counter per
+    128-byte line) at the next 256-byte boundary."""
+    bias = b * h * n * 4 if score else 0
+    return (bias + 255) // 256 * 256 + 2048
+
+
+def _run(q, k, v, causal, weighted, decay, window, use_ws, ws_bytes=None, score=True):
     b, h, n, d = q.shape
     hk = k.shape[1]
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -28,13 +36,15 @@ def _run(q, k, v, causal, weighted, decay, window, use_ws):
     L = _lib.lib()
     w = min(n, window or n)
     stream = torch.cuda.current_stream().cuda_stream
-    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), b, h, hk, n, d,
-            _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], d ** -0.5, int(causal),
-            int(weighted), 1, decay, w)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr() if score else None, b, h, hk,
+            n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], d ** -0.5, int(causal),
+            int(weighted), int(score), decay, w)
     if use_ws:
-        nbytes = L.fe_prefill_workspace_bytes(b, h, n, 1)
-        assert nbytes == b * h * n * 4
-        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        nbytes = L.fe_prefill_workspace_bytes(b, h, n, int(score))
+        assert nbytes == _ws_layout(b, h, n, score)
+        if ws_bytes is not None:
+            nbytes = ws_bytes
+        ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=q.device)
         rc = L.fe_prefill_ws(*args, ws.data_ptr(), nbytes, stream)
     else:
         rc = L.fe_prefill(*args, stream)
@@ -86,3 +96,24 @@ def test_small_workspace_falls_back_to_fused():
     assert torch.equal(out, o1)
     # same fused kernel; only the FP32 atomic order can differ between the two runs
     assert float((imp - i1).abs().max()) <= 2e-6 * float(i1.abs().max())
+
+
+@pytest.mark.parametrize("b,hq,hk,n,d,dtype,causal,weighted,decay,window,layout", CASES)
+def test_dynamic_and_static_schedules_agree(b, hq, hk, n, d, dtype, causal, weighted, decay, window, layout):
+    """The dynamic schedule (the whole workspace: work items taken from a counter, heaviest
+    first) against the static one (a workspace of the replay biases only: item = workgroup
+    index). Each item is computed the same way whichever workgroup takes it, so the output is
+    bitwise equal, with and without scoring, and the importance equal up to FP32 atomic order."""
+    print(f"dynamic vs static b={b} hq={hq} hk={hk} n={n} d={d} {dtype} causal={causal} window={window}", flush=True)
+    q = seeded_randn((b, hq, n, d), dtype, 3 * n + d)
+    k = seeded_randn((b, hk, n, d), dtype, 3 * n + d + 1)
+    v = seeded_randn((b, hk, n, d), dtype, 3 * n + d + 2)
+    o_dyn, i_dyn = _run(q, k, v, causal, weighted, decay, window, use_ws=True)
+    o_st, i_st = _run(q, k, v, causal, weighted, decay, window, use_ws=True, ws_bytes=b * hq * n * 4)
+    assert torch.equal(o_dyn, o_st)
+    assert float((i_dyn - i_st).abs().max()) <= 3e-6 * float(i_st.abs().max())
+    # attention only: counters alone (dynamic) against no workspace (static)
+    o_dyn0, _ = _run(q, k, v, causal, weighted, decay, window, use_ws=True, score=False)
+    o_st0, _ = _run(q, k, v, causal, weighted, decay, window, use_ws=True, ws_bytes=0, score=False)
+    assert torch.equal(o_dyn0, o_st0)
+    assert torch.equal(o_dyn0, o_dyn)
