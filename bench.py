@@ -1,9 +1,12 @@
 """Benchmark of the flash_evict prefill hot path on one MI355X.
 
 A step is one full `evict()` layer (zero-init, attention kernel + replay kernel, value-norm
-scaling, radix top-k + mask) over resident synthetic bf16 inputs at the headline shape B=1,
-Hq=32, Hkv=8, N=32768, D=128, causal, budget 1024, recency_decay 0.1, reserved_recent 64,
-all-query window (observation_window 0).
+scaling, radix top-k + mask) over resident synthetic inputs. The default is the headline shape
+B=1, Hq=32, Hkv=8, N=32768, D=128, bf16, causal, budget 1024, recency_decay 0.1,
+reserved_recent 64, all-query window (observation_window 0); --config selects the other
+BASELINE configs (tiny and edge in fp16, llama8k, qwen32k_w128, long131k), the headline in
+fp16, the reference harness's default shape (ref8k, ref32k, ref128k) and D=64 at the headline
+head counts (d64_b10).
 
 Work counts. The metric's definition of a layer's work is 4*D*P_attn + 2*D*P_replay with
 P_attn = B*Hq*N(N+1)/2 (causal) and P_replay the query-key pairs of the last W query rows
@@ -35,21 +38,75 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "flash-evict-prefill_amd"), ROOT]
 
-PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 (and fp16) MFMA (published)
 
+# name: shape, element type, input recipe and evict() arguments. The first five after the
+# headline are the BASELINE.json configs (tiny and edge in fp16); headline_f16 is the headline
+# in fp16; ref8k/ref32k/ref131k are the reference harness's default shape (scripts/benchmark.py:
+# Hq4/Hkv2/D64 bf16, budget ceil(0.1 N), default scoring: every row replayed); d64_b10 is D=64
+# at the headline head counts with every row replayed.
+_HL = dict(B=1, Hq=32, Hkv=8, N=32768, D=128)
+_HL_EVICT = dict(budget=1024, recency_decay=0.1, reserved_recent=64, observation_window=0, pool_kernel=1)
 CONFIGS = {
-    # name: (B, Hq, Hkv, N, D, evict kwargs)
-    "headline": (1, 32, 8, 32768, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
-                                            observation_window=0, pool_kernel=1)),
-    "headline_b10": (1, 32, 8, 32768, 128, dict(budget=3277, recency_decay=0.0, reserved_recent=0,
-                                                observation_window=0, pool_kernel=1)),
-    "llama8k": (1, 32, 8, 8192, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
-                                          observation_window=0, pool_kernel=1)),
-    "qwen32k_w128": (1, 28, 4, 32768, 128, dict(budget=2048, recency_decay=0.0, reserved_recent=64,
-                                                observation_window=128, pool_kernel=5)),
-    "long131k": (1, 32, 8, 131072, 128, dict(budget=1024, recency_decay=0.1, reserved_recent=64,
-                                             observation_window=0, pool_kernel=1)),
+    "headline": dict(_HL, dtype="bf16", evict=_HL_EVICT),
+    "tiny": dict(B=1, Hq=4, Hkv=4, N=512, D=64, dtype="f16",
+                 evict=dict(budget=64, recency_decay=0.0, reserved_recent=0, observation_window=0, pool_kernel=1)),
+    "edge": dict(B=2, Hq=8, Hkv=2, N=4000, D=128, dtype="f16", causal=False, value_weighted=False, qk_scale=30.0,
+                 transposed=True, zero_v_rows=0.1,
+                 evict=dict(budget=400, recency_decay=0.0, reserved_recent=0, observation_window=0, pool_kernel=1)),
+    "llama8k": dict(B=1, Hq=32, Hkv=8, N=8192, D=128, dtype="bf16", outlier_channels=4,
+                    evict=dict(budget=1024, recency_decay=0.1, reserved_recent=64, observation_window=0, pool_kernel=1)),
+    "qwen32k_w128": dict(B=1, Hq=28, Hkv=4, N=32768, D=128, dtype="bf16",
+                         evict=dict(budget=2048, recency_decay=0.0, reserved_recent=64, observation_window=128,
+                                    pool_kernel=5)),
+    "long131k": dict(B=1, Hq=32, Hkv=8, N=131072, D=128, dtype="bf16",
+                     evict=dict(budget=1024, recency_decay=0.1, reserved_recent=64, observation_window=0, pool_kernel=1)),
+    "headline_f16": dict(_HL, dtype="f16", evict=_HL_EVICT),
+    "headline_b10": dict(_HL, dtype="bf16", evict=dict(budget=3277, recency_decay=0.0, reserved_recent=0,
+                                                        observation_window=0, pool_kernel=1)),
+    "d64_b10": dict(B=1, Hq=32, Hkv=8, N=32768, D=64, dtype="bf16",
+                    evict=dict(budget=3277, recency_decay=0.0, reserved_recent=0, observation_window=0, pool_kernel=1)),
 }
+for _n in (8192, 32768, 131072):
+    CONFIGS["ref%dk" % (_n // 1024)] = dict(B=1, Hq=4, Hkv=2, N=_n, D=64, dtype="bf16",
+                                           evict=dict(budget=-(-_n // 10), recency_decay=0.0, reserved_recent=0,
+                                                      observation_window=0, pool_kernel=1))
+
+
+def kernel_names(cfg):
+    """The attention and replay kernels the split schedule runs for a config (fast layouts):
+    the two-row-tile attention kernel at tile dims 96 and 128, else the one-row-tile one."""
+    e = cfg["dtype"]
+    dp = -(-cfg["D"] // 32) * 32
+    part = "" if dp == cfg["D"] else ",partial"
+    attn = "attn_rt2" if dp in (96, 128) else "attn_fast"
+    return "%s<%s,%d%s>" % (attn, e, dp, part), "replay_fast<%s,%d%s>" % (e, dp, part)
+
+
+def make_inputs(cfg, dev):
+    """Seeded synthetic q, k, v of the config, resident on `dev` (drawn on the device)."""
+    import torch
+    dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float16
+    b, hq, hk, n, d = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["N"], cfg["D"]
+    gen = torch.Generator(device=dev).manual_seed(20260910)
+    if cfg.get("transposed"):
+        q = torch.randn((b, n, hq, d), device=dev, generator=gen).transpose(1, 2)
+        k = torch.randn((b, n, hk, d), device=dev, generator=gen).transpose(1, 2)
+        v = torch.randn((b, n, hk, d), device=dev, generator=gen).transpose(1, 2)
+    else:
+        q = torch.randn((b, hq, n, d), device=dev, generator=gen)
+        k = torch.randn((b, hk, n, d), device=dev, generator=gen)
+        v = torch.randn((b, hk, n, d), device=dev, generator=gen)
+    s = cfg.get("qk_scale", 1.0)
+    q, k = q * s, k * s
+    if cfg.get("outlier_channels"):
+        ch = torch.randperm(d, generator=gen, device=dev)[: cfg["outlier_channels"]]
+        q[..., ch] *= 8
+        k[..., ch] *= 8
+    if cfg.get("zero_v_rows"):
+        rows = torch.randperm(n, generator=gen, device=dev)[: int(n * cfg["zero_v_rows"])]
+        v[:, :, rows] = 0
+    return q.to(dt), k.to(dt), v.to(dt)
 
 
 def log(msg):
@@ -123,8 +180,8 @@ def cpu_baseline(q, k, v, kw, executed_flop, sample_heads=8):
     sample_heads = min(sample_heads, hq)
     kv_needed = (sample_heads + g - 1) // g
     qc, kc, vc = q[:1, :sample_heads].cpu(), k[:1, :kv_needed].cpu(), v[:1, :kv_needed].cpu()
-    args = dict(causal=True, value_weighted=True, recency_decay=kw["recency_decay"],
-                observation_window=kw["observation_window"], block=1024)
+    args = dict(causal=kw.get("causal", True), value_weighted=kw.get("value_weighted", True),
+                recency_decay=kw["recency_decay"], observation_window=kw["observation_window"], block=1024)
     chunked(qc, kc, vc, heads=[(0, 0)], query_rows=[(0, 2048)], **args)        # warm-up
     t0 = time.perf_counter()
     _, imp = chunked(qc, kc, vc, **args)
@@ -205,39 +262,43 @@ def main():
     import torch
     import flash_evict
 
-    b, hq, hk, n, d, kw = CONFIGS[args.config]
+    cfg = CONFIGS[args.config]
+    b, hq, hk, n, d = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["N"], cfg["D"]
+    causal, weighted = cfg.get("causal", True), cfg.get("value_weighted", True)
+    kw = dict(cfg["evict"], causal=causal, value_weighted=weighted)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    log("config %s: B=%d Hq=%d Hkv=%d N=%d D=%d %s" % (args.config, b, hq, hk, n, d, kw))
-    gen = torch.Generator(device=dev).manual_seed(20260910)
-    q = torch.randn((b, hq, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
-    k = torch.randn((b, hk, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
-    v = torch.randn((b, hk, n, d), device=dev, dtype=torch.bfloat16, generator=gen)
+    log("config %s: B=%d Hq=%d Hkv=%d N=%d D=%d %s %s" % (args.config, b, hq, hk, n, d, cfg["dtype"], kw))
+    q, k, v = make_inputs(cfg, dev)
     torch.cuda.synchronize()
 
     def make_step(decay):
         def step():
             return flash_evict.evict(q, k, v, kw["budget"], reserved_recent=kw["reserved_recent"],
                                      pool_kernel=kw["pool_kernel"], recency_decay=decay,
-                                     observation_window=kw["observation_window"])
+                                     observation_window=kw["observation_window"], causal=causal,
+                                     value_weighted=weighted)
         return step
+
+    def flops(decay, effective=True):
+        return algorithmic_flop(b, hq, n, d, kw["observation_window"], decay, causal=causal, effective=effective)
 
     with torch.inference_mode():
         ms, fused_avg_ms, launches = _timed_layers(make_step(kw["recency_decay"]), args.steps, args.warmup,
-                                                   "headline")
+                                                   args.config)
         full = None
         if kw["recency_decay"] > 0 and not args.no_full_replay:
             fsteps = max(3, args.steps // 2)
             f_ms, f_fused, f_launches = _timed_layers(make_step(0.0), fsteps, min(2, args.warmup), "full-replay")
-            f_flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], 0.0)
+            f_flop = flops(0.0)
             f_ach = f_flop / (f_fused * 1e-3) / 1e12
             full = {"recency_decay": 0.0, "replay_rows": replay_rows(n, kw["observation_window"], 0.0),
                     "executed_tflop": round(f_flop / 1e12, 4), "ms_per_layer": round(f_ms, 4),
                     "fused_mean_ms": round(f_fused, 4), "fused_achieved_tflops": round(f_ach, 2),
                     "fused_frac": round(f_ach / PEAK_BF16_TFLOPS, 4), "launches": f_launches,
                     "steps": fsteps}
-    flop = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"], effective=False)
-    executed = algorithmic_flop(b, hq, n, d, kw["observation_window"], kw["recency_decay"])
+    flop = flops(kw["recency_decay"], effective=False)
+    executed = flops(kw["recency_decay"])
     achieved = executed / (fused_avg_ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(args.traffic_json):
@@ -248,6 +309,7 @@ def main():
                 traffic = tj.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
+    attn_name, replay_name = kernel_names(cfg)
     record = {
         "metric": "ms/layer + fused attn+score TFLOP/s (% MFMA peak), N=32K Hq32/Hkv8 D128 bf16",
         "value": round(executed / (ms * 1e-3) / 1e12, 2),
@@ -259,16 +321,22 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v resident in HBM)",
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded normal q/k/v resident in HBM%s)" % (
+            "; q,k x%g, %s" % (cfg.get("qk_scale", 1.0), ", ".join(x for x in (
+                "transposed [B,N,H,D] views" if cfg.get("transposed") else "",
+                "%d%% zero v rows" % int(100 * cfg["zero_v_rows"]) if cfg.get("zero_v_rows") else "",
+                "%d outlier channels x8" % cfg["outlier_channels"] if cfg.get("outlier_channels") else "") if x))
+            if any(cfg.get(x) for x in ("transposed", "zero_v_rows", "outlier_channels", "qk_scale")) else ""),
         "config": {"workload": "evict() layer, %s" % args.config, "B": b, "Hq": hq, "Hkv": hk, "N": n, "D": d,
-                   "causal": True, **kw, "algorithmic_tflop": round(flop / 1e12, 4),
+                   **kw, "algorithmic_tflop": round(flop / 1e12, 4),
                    "replay_rows": replay_rows(n, kw["observation_window"], kw["recency_decay"]),
                    "executed_tflop": round(executed / 1e12, 4)},
         "value_defined_work": round(flop / (ms * 1e-3) / 1e12, 2),
-        "roofline": {"bound": "mfma", "kernel": "fused_attn_score", "achieved": round(achieved, 2),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic, "mean_ms": round(fused_avg_ms, 4), "launches": launches},
+        "roofline": {"bound": "mfma", "kernel": "%s + %s" % (attn_name, replay_name),
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "mean_ms": round(fused_avg_ms, 4), "launches": launches},
         "fused_share_of_layer": round(fused_avg_ms / ms, 4),
         "full_replay": full,
     }

@@ -886,16 +886,16 @@ namespace {
 // a fill kernel) before its kernels run.
 __device__ __align__(256) float scratch[FE_STATIC_BIAS_ROWS + kQueueWords];
 
-// Device address of `scratch`, per device: looked up once per device, with that device
-// current, on the first fe_prefill_static call that runs on it. Host code passes this
-// address to the kernels; the array's name is only a host-side stand-in symbol.
-struct ScratchSlot {
-  std::once_flag once;
-  void* ptr = nullptr;
-  hipError_t err = hipSuccess;
-};
+// Device address of `scratch`, per device: looked up with that device current, on the first
+// fe_prefill_static call that runs there, and kept. Host code passes this address to the
+// kernels; the array's name is only a host-side stand-in symbol. Only a successful lookup is
+// kept: a failed one (say, a call made while the device was busy with another context)
+// returns its error and the next call tries again. The lookup (and the first call's occupancy
+// queries) are host API calls, not stream work; a caller that captures fe_prefill_static in a
+// HIP graph makes one eager call on each device first, so the capture finds them done.
 constexpr int kMaxDevices = 64;
-ScratchSlot g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
 
 hipError_t static_scratch(hipStream_t stream, float** out) {
   int cur = 0;
@@ -908,18 +908,20 @@ hipError_t static_scratch(hipStream_t stream, float** out) {
     dev = (int)d;
   }
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  ScratchSlot& slot = g_scratch[dev];
-  std::call_once(slot.once, [&] {
-    if (dev != cur && (slot.err = hipSetDevice(dev)) != hipSuccess) return;
-    slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    if (dev != cur && (err = hipSetDevice(dev)) != hipSuccess) return err;
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (dev != cur) {
       const hipError_t back = hipSetDevice(cur);
-      if (slot.err == hipSuccess) slot.err = back;
+      if (err == hipSuccess) err = back;
     }
-    if (slot.err == hipSuccess && !slot.ptr) slot.err = hipErrorInvalidSymbol;
-  });
-  if (slot.err != hipSuccess) return slot.err;
-  *out = (float*)slot.ptr;
+    if (err != hipSuccess) return err;
+    if (!ptr) return hipErrorInvalidSymbol;
+    g_scratch[dev] = ptr;
+  }
+  *out = (float*)g_scratch[dev];
   return hipSuccess;
 }
 

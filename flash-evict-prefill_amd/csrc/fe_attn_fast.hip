@@ -368,7 +368,7 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
     // probabilities may exceed 1 where the row's max has risen. The output is O divided by
     // l_rnd, the sum of the probabilities exactly as rounded for the P@V product, so a row
     // dominated by one key returns that key's value whatever m is (dividing by the unrounded
-    // sum would leave that key's rounding error, up to 2^-9 relative in bf16, in the output).
+    // sum would leave that key's rounding error, up to 2^-8 relative in bf16, in the output).
     // The replay bias needs the FP32 sum of the unrounded probabilities (l_run, replay rows
     // only): b = m + log2 l_run does not depend on the choice of m. A tile some lane of which
     // sums to more than E::kMaxTileSum (inf included) takes a new exact max, rescales O and

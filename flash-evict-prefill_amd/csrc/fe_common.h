@@ -19,9 +19,15 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // Element tags: storage is always 16-bit; the tag selects MFMA flavour and rounding.
 struct BF16 {
   typedef __bf16 scalar;
-  // Largest per-lane sum of one tile's probabilities (relative to a row's reference max)
+  // Largest per-lane sum of one step's probabilities (relative to a row's reference max)
   // the attention kernels accept before taking a new reference max: bf16 and the FP32
-  // accumulation have FP32's range, and 2^32 leaves room for long rows of large values.
+  // accumulation have FP32's range. A row then gains at most 2 * 2^32 per 32 keys (two
+  // lanes hold its keys), so its sum stays below 2^33 * ceil(N/32) and |O| below that times
+  // max|v|: O stays finite for max|v| < 2^95 / ceil(N/32) (2^83, about 1e25, at N = 131072).
+  // The reference's running max keeps every probability at most 1, so its accumulator stays
+  // finite up to max|v| < 2^128 / N. Between the two bounds the output overflows here and
+  // not there; below 2^95 / ceil(N/32) every rounding is relative, and scaling V by a power
+  // of two scales the output and importance exactly.
   static constexpr float kMaxTileSum = 4294967296.f;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -54,7 +60,8 @@ struct BF16 {
 
 struct F16 {
   typedef _Float16 scalar;
-  static constexpr float kMaxTileSum = 32768.f;  // probabilities stay below the fp16 maximum
+  // probabilities stay below the fp16 maximum; |O| < 2^16 * ceil(N/32) * 65504 is always finite
+  static constexpr float kMaxTileSum = 32768.f;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);

@@ -12,12 +12,18 @@ tile, after the first 32 keys):
   * a jump of ~2^20 (below the guard): the dominant key's probability is far from 1 and is
     rounded to bf16. With the rounded-sum normalisation the output of every dominated row
     equals that key's value row bit for bit; dividing by the unrounded sum instead would
-    leave the probability's rounding error (up to 2^-9 relative) in the output, which
+    leave the probability's rounding error (up to 2^-8 relative) in the output, which
     changes some of these bf16 outputs by an ulp;
   * a jump of ~2^56 (above the guard): the tile takes a new exact max and is recomputed;
     the same bitwise property holds;
   * fp16, whose guard is 2^15, across both regimes: output and importance against the
-    float64 oracle.
+    float64 oracle;
+  * head dim 120 (the two-row-tile kernel below its tile dim, lanes past channel 120 reading
+    zeros) with an observation window of 100 rows, so that the waves holding earlier rows take
+    the tile loop without the FP32 sum, in bf16 and fp16 across both regimes;
+  * values scaled by 2^60: every rounding in the kernel is relative, so the output and the
+    importance scale by exactly 2^60 (the bound on |V| under which the accumulators stay
+    finite is in fe_common.h).
 
 Importance is checked element-wise against the oracle in every case.
 """
@@ -87,3 +93,37 @@ def test_dominant_key_after_first_tile_fp16(jump_log2, d, kp):
     ref_out, ref_imp = chunked(q, k, v, block=512, dtype=torch.float64)
     assert (out.float() - ref_out).abs().max().item() <= 5e-3
     assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+
+
+@pytest.mark.parametrize("dtype,jump_log2", [(torch.bfloat16, 24.0), (torch.bfloat16, 60.0),
+                                             (torch.float16, 10.0), (torch.float16, 30.0)])
+def test_dominant_key_partial_head_dim_short_window(dtype, jump_log2):
+    n, hq, hk, d, kp, window = 1024, 4, 2, 120, 300, 100
+    print("planted dominant key %s: n=%d d=%d kp=%d jump 2^%g window %d" % (dtype, n, d, kp, jump_log2, window),
+          flush=True)
+    q, k, v = _planted(n, hq, hk, d, dtype, kp, jump_log2, seed=13)
+    out, imp = prefill(q, k, v, observation_window=window)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(imp).all()
+    ref_out, ref_imp = chunked(q, k, v, block=512, dtype=torch.float64, observation_window=window)
+    bar = 2e-2 if dtype == torch.bfloat16 else 5e-3
+    assert (out.float() - ref_out).abs().max().item() <= bar
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    if dtype == torch.bfloat16:
+        # every row that sees key kp returns its KV head's value row of kp exactly
+        want = v[0, torch.arange(hq) // (hq // hk), kp]           # [hq, d]
+        dom = out[0, :, kp:, :]
+        assert bool((dom == want[:, None, :].expand_as(dom)).all())
+
+
+@pytest.mark.parametrize("use_ws", [True, False])
+def test_large_values_scale_exactly(use_ws):
+    n, hq, hk, d, kp = 1024, 2, 1, 128, 300
+    q, k, v = _planted(n, hq, hk, d, torch.bfloat16, kp, 24.0, seed=14)
+    s = 2.0 ** 60
+    out1, imp1 = _run(q, k, v, True, True, 0.0, 0, use_ws=use_ws)
+    out2, imp2 = _run(q, k, v * s, True, True, 0.0, 0, use_ws=use_ws)
+    assert torch.isfinite(out2).all() and torch.isfinite(imp2).all()
+    assert torch.equal(out2, out1 * s)
+    # the importance is the value-weighted mass: exactly 2^60 times, up to FP32 atomic order
+    assert float((imp2 / s - imp1).abs().max()) <= 3e-6 * float(imp1.abs().max())

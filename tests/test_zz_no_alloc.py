@@ -89,6 +89,49 @@ def test_static_entry_without_score_and_at_head_dim_96():
     assert torch.equal(out, out_w)
 
 
+@pytest.mark.gpu
+def test_static_entry_under_graph_capture_allocates_nothing():
+    """fe_prefill_static for a caller that cannot allocate: one eager call (it looks up the
+    static buffer and the kernels' occupancy on this device), more eager calls that leave the
+    device's free memory unchanged, then the call captured in a HIP graph (torch.cuda.CUDAGraph)
+    and replayed three times with eager work and synchronisations between the replays. The
+    eager calls and every replay match fe_prefill_ws: bitwise output, importance up to FP32
+    atomic order (each replay zeroes the importance and the work-item counters with fill kernels,
+    not memset nodes)."""
+    b, hq, hk, n, d = 1, 8, 2, 2048, 128
+    print("fe_prefill_static under graph capture: B=%d Hq=%d Hkv=%d N=%d D=%d bf16" % (b, hq, hk, n, d), flush=True)
+    q, k, v = transposed_qkv(b, n, hq, hk, d, torch.bfloat16, 20261210)
+    out_w, imp_w = _run(q, k, v, True, True, 0.05, 0, static=False)
+    tol = 2e-6 * imp_w.abs() + 1e-6 * imp_w.abs().amax(-1, keepdim=True)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    imp = torch.empty((b, hk, n), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    args = _args(q, k, v, out, imp, True, True, 0.05, 0)
+    _lib.check(L.fe_prefill_static(*args, torch.cuda.current_stream().cuda_stream), "fe_prefill_static")
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        _lib.check(L.fe_prefill_static(*args, torch.cuda.current_stream().cuda_stream), "fe_prefill_static")
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.equal(out, out_w)
+    assert bool(((imp - imp_w).abs() <= tol).all())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = L.fe_prefill_static(*args, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "fe_prefill_static (captured)")
+    for r in range(3):
+        out.zero_()
+        imp.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print("replay %d" % r, flush=True)
+        assert torch.equal(out, out_w)
+        assert bool(((imp - imp_w).abs() <= tol).all())
+    del g
+
+
 def test_static_entry_rejects_sizes_beyond_its_buffer():
     """B*Hq*N above FE_STATIC_BIAS_ROWS fails with FE_ERR_WORKSPACE before any HIP call
     (the pointers below are never dereferenced)."""
