@@ -19,7 +19,9 @@ struct AttnArgs {
   float* imp;
   float* bias;                      // split schedule: per-row replay bias out of traversal 1 (else null)
   long long qs[4], ks[4], vs[4];   // element strides {b, h, n, d}
-  int N, D, G, Hq, Hkv, BH;
+  int N, D, G, Hq, Hkv, BH;           // D: channels of the K/V rows the kernel reads
+  int Dq;                           // channels of Q and out (D, or less when K/V were repacked)
+  unsigned qmask;                   // ANDed into Q at load: 0 runs a zero scale on the fast kernels
   int tiles_bh;                     // row tiles per (b, kv head): G * ceil(N/32)
   int wg_bh;                        // workgroups per (b, kv head)
   float scale_log2;                 // softmax scale * log2(e)
@@ -74,6 +76,9 @@ struct FusedPlan {
 // Fast path (fe_attn_fast.hip): D a multiple of 8 up to 256, nonzero scale, 16-byte unit-stride
 // buffer-addressable K/V rows (Q of any strides). Returns false (and leaves `plan` untouched) when it does not apply.
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan);
+// Whether the fast kernels can read K and V as laid out (D a multiple of 8 up to 256; aligned,
+// unit-stride rows within 32-bit byte offsets).
+bool fast_layout(const AttnArgs& a);
 // Replay kernel of the split schedule (fe_attn_fast.hip): same layout rules as fast_plan;
 // launched with ReplayPlan::waves waves and ReplayPlan::rows row tiles per workgroup.
 struct ReplayPlan {

@@ -483,6 +483,43 @@ hipError_t launch_zero(float* p, int64_t n, int* ctr, int nctr, hipStream_t stre
 
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t stream) { return launch_zero(p, n, nullptr, 0, stream); }
 
+// K or V rows that the fast kernels' tile DMA cannot read (rows off 16-byte alignment, a
+// channel stride other than 1, a broadcast, a head dim not a multiple of 8), copied into the
+// caller's workspace: out[b, h, n, 0:Dp) = x[b, h, n, 0:D) (element strides s0..s3, any
+// alignment) and zero in D..Dp-1, Dp = D rounded up to 8, rows contiguous. One 16-byte chunk
+// of eight channels per thread.
+__global__ __launch_bounds__(256) void repack_rows_kernel(const u16* x, long long s0, long long s1, long long s2,
+                                                          long long s3, int H, int N, int D, int Dp, u16* out,
+                                                          long long chunks) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int cpr = Dp >> 3;
+  const long long row = i / cpr;
+  const int c = (int)(i - row * cpr);
+  const long long bh = row / N;
+  const int n = (int)(row - bh * N);
+  const long long b = bh / H, h = bh - b * H;
+  const u16* p = x + b * s0 + h * s1 + (long long)n * s2;
+  *(u32x4*)(out + row * Dp + 8 * c) = load8(p, s3, 8 * c, D, 0);
+}
+
+hipError_t launch_repack(const u16* x, const int64_t* st, int64_t B, int64_t H, int64_t N, int64_t D, int64_t Dp,
+                         u16* out, hipStream_t stream) {
+  const long long chunks = (long long)(B * H * N) * (Dp / 8);
+  const long long blocks = (chunks + 255) / 256;
+  hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, (long long)st[0],
+                     (long long)st[1], (long long)st[2], (long long)st[3], (int)H, (int)N, (int)D, (int)Dp, out,
+                     chunks);
+  return hipGetLastError();
+}
+
+// Bytes of one repacked K or V area: B*Hkv*N rows of Dp = D rounded up to 8 channels, 256-byte
+// aligned.
+size_t repack_bytes(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
+  const size_t b = (size_t)(B * Hkv * N) * (size_t)((D + 7) / 8 * 8) * 2;
+  return (b + 255) & ~(size_t)255;
+}
+
 namespace {
 
 // Workgroups of a kernel that the device holds at once: the CU count times the kernel's
@@ -691,6 +728,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   }
   a.N = (int)N;
   a.D = (int)D;
+  a.Dq = (int)D;
+  a.qmask = 0xffffffffu;
   a.G = (int)G;
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
@@ -713,9 +752,31 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   FusedPlan plan;
   ReplayPlan rplan;
   // Workspace: the replay bias of every query row (scoring calls), then the dynamic
-  // schedule's item counters at the next 256-byte boundary.
+  // schedule's item counters at the next 256-byte boundary, then (K/V layouts the fast kernels
+  // cannot read) the repacked K and V.
   const size_t ws_bias = score ? (size_t)(B * Hq * N) * sizeof(float) : 0;
   const size_t ws_ctr = (ws_bias + 255) & ~(size_t)255;
+  const size_t ws_kv = ws_ctr + kQueueBytes, kv_bytes = repack_bytes(B, Hkv, N, D);
+  const bool repack = !fast_layout(a) && workspace && workspace_bytes >= ws_kv + 2 * kv_bytes;
+  if (repack) {
+    const int64_t Dp = (D + 7) / 8 * 8;
+    AttnArgs r = a;
+    r.k = (const u16*)((char*)workspace + ws_kv);
+    r.v = (const u16*)((char*)workspace + ws_kv + kv_bytes);
+    const long long st[4] = {(long long)(Hkv * N * Dp), (long long)(N * Dp), (long long)Dp, 1};
+    for (int i = 0; i < 4; ++i) r.ks[i] = r.vs[i] = st[i];
+    r.D = (int)Dp;
+    r.kvec = r.vvec = 1;
+    if (fast_layout(r)) a = r;
+  }
+  // A zero scale runs on the fast kernels with Q zeroed at load: every logit is then exactly
+  // 0 (the reference's 0 * (q.k) for finite q.k), and masked keys stay at -inf.
+  if (!(a.abs_scale_log2 > 0.f)) {
+    AttnArgs z = a;
+    z.qmask = 0;
+    z.abs_scale_log2 = 1.f;
+    if (fast_plan(z, dtype, plan)) a = z;
+  }
   const bool split = score && workspace && workspace_bytes >= ws_bias && replay_plan(a, dtype, rplan);
   if (split) a.bias = (float*)workspace;
   bool fast = fast_plan(a, dtype, plan);
@@ -756,6 +817,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     err = launch_zero(score ? importance : nullptr, score ? B * Hkv * N : 0, ctr, ctr ? kQueueWords : 0, stream);
     if (err != hipSuccess) {
       set_error(std::string("fe_prefill: zero-init launch: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+  }
+  if (a.k != (const u16*)k) {
+    err = launch_repack((const u16*)k, k_strides, B, Hkv, N, D, a.D, (u16*)a.k, stream);
+    if (err == hipSuccess) err = launch_repack((const u16*)v, v_strides, B, Hkv, N, D, a.D, (u16*)a.v, stream);
+    if (err != hipSuccess) {
+      set_error(std::string("fe_prefill: K/V repack launch: ") + hipGetErrorString(err));
       return FE_ERR_HIP;
     }
   }
@@ -824,16 +893,18 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     ev.e[0] = ev.e[1] = nullptr;
   }
   if (score && value_weighted) {
+    // the caller's V (a repacked copy may be what the attention kernels read)
+    const int vvec = vec_ok(v, v_strides, D);
     const long long rows = B * Hkv * N;
     const long long nb = (rows + 31) / 32;
     if (dtype == FE_DTYPE_BF16)
       hipLaunchKernelGGL(value_l1_scale_kernel<BF16>, dim3((unsigned)nb), dim3(256), 0, stream, (const u16*)v,
                          (long long)v_strides[0], (long long)v_strides[1], (long long)v_strides[2],
-                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, a.vvec, importance, rows);
+                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, vvec, importance, rows);
     else
       hipLaunchKernelGGL(value_l1_scale_kernel<F16>, dim3((unsigned)nb), dim3(256), 0, stream, (const u16*)v,
                          (long long)v_strides[0], (long long)v_strides[1], (long long)v_strides[2],
-                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, a.vvec, importance, rows);
+                         (long long)v_strides[3], (int)Hkv, (int)N, (int)D, vvec, importance, rows);
     err = hipGetLastError();
     if (err != hipSuccess) {
       set_error(std::string("fe_prefill: value-norm launch: ") + hipGetErrorString(err));
@@ -863,6 +934,24 @@ extern "C" size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, i
   if (B < 1 || Hq < 1 || N < 1) return 0;
   const size_t bias = score ? (size_t)(B * Hq * N) * sizeof(float) : 0;
   return ((bias + 255) & ~(size_t)255) + kQueueBytes;
+}
+
+extern "C" size_t fe_prefill_workspace_bytes_kv(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int score,
+                                                const void* k, const int64_t* k_strides, const void* v,
+                                                const int64_t* v_strides) {
+  const size_t base = fe_prefill_workspace_bytes(B, Hq, N, score);
+  if (base == 0 || Hkv < 1 || D < 1 || D > 256 || !k || !v || !k_strides || !v_strides || N > (1LL << 30)) return base;
+  AttnArgs a = {};
+  a.k = (const u16*)k;
+  a.v = (const u16*)v;
+  for (int i = 0; i < 4; ++i) {
+    a.ks[i] = k_strides[i];
+    a.vs[i] = v_strides[i];
+  }
+  a.N = (int)N;
+  a.D = (int)D;
+  if (fast_layout(a)) return base;
+  return base + 2 * repack_bytes(B, Hkv, N, D);
 }
 
 extern "C" int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,

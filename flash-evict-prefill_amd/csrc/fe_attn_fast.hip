@@ -118,6 +118,21 @@ __device__ __forceinline__ void dma_tile_cm(const unsigned char* g, u32 rowb, u3
   }
 }
 
+// Four consecutive output channels d0 .. d0+3 of one row (w0: d0, d0+1; w1: d0+2, d0+3). Below
+// the tile dim (PARTIAL) the row holds Dq channels: a group past Dq is not stored, and where Dq
+// is not a multiple of 4 (rows then not 8-byte aligned) the channels are stored one by one.
+template <bool PARTIAL>
+__device__ __forceinline__ void store4(u16* op, int d0, int Dq, u32 w0, u32 w1) {
+  if (!PARTIAL || ((Dq & 3) == 0 && d0 + 4 <= Dq)) {
+    *(u32x2*)(op + d0) = (u32x2){w0, w1};
+    return;
+  }
+  const u16 h[4] = {(u16)w0, (u16)(w0 >> 16), (u16)w1, (u16)(w1 >> 16)};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (d0 + e < Dq) op[d0 + e] = h[e];
+}
+
 // The lane's index, recomputed where it is used: opaque to the compiler, which would
 // otherwise keep values derived from it live across a loop and, at two or three waves per
 // SIMD, spill them (each reload then waits behind the next tile's DMA).
@@ -284,7 +299,7 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
       const bool ok = tv && qr < N;
       const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
   #pragma unroll
-      for (int c = 0; c < NDC; ++c) qf[c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+      for (int c = 0; c < NDC; ++c) qf[c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     }
 
     // Per-lane LDS byte offsets, one per operand, fixed for the kernel. The fragment, key
@@ -560,16 +575,16 @@ __global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fuse
       const int qi = q0 + l32;
       if (tv && qi < N) {
         const float inv = 1.f / half_swap_sum(l_rnd);
-        u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * (PARTIAL ? a.D : DP);
+        u16* op = a.out + ((long long)(b * a.Hq + head) * N + qi) * (PARTIAL ? a.Dq : DP);
   #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
   #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const int d0 = 32 * dt + 8 * g4 + 4 * hh;
-            if (PARTIAL && d0 >= a.D) continue;    // channels past D (a multiple of 8) are not stored
+            if (PARTIAL && d0 >= a.Dq) continue;   // channels past Q's head dim are not stored
             const u32 w0 = E::pack2(o[dt][4 * g4 + 0] * inv, o[dt][4 * g4 + 1] * inv);
             const u32 w1 = E::pack2(o[dt][4 * g4 + 2] * inv, o[dt][4 * g4 + 3] * inv);
-            *(u32x2*)(op + d0) = (u32x2){w0, w1};
+            store4<PARTIAL>(op, d0, a.Dq, w0, w1);
           }
         }
       }
@@ -781,7 +796,7 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       const u16* qp = a.q + b * a.qs[0] + head[j] * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
   #pragma unroll
       for (int c = 0; c < NDC; ++c)
-        qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+        qf[j][c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     }
 
     // LDS operand offsets and tile DMA: the layout of fused_fast_kernel
@@ -1034,16 +1049,16 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       const float inv = 1.f / half_swap_sum(l_rnd[j]);
       const int qi = q0[j] + l32;
       if (tv[j] && qi < N) {
-        u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * (PARTIAL ? a.D : DP);
+        u16* op = a.out + ((long long)(b * a.Hq + head[j]) * N + qi) * (PARTIAL ? a.Dq : DP);
   #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
   #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const int d0 = 32 * dt + 8 * g4 + 4 * hh;
-            if (PARTIAL && d0 >= a.D) continue;
+            if (PARTIAL && d0 >= a.Dq) continue;
             const u32 w0 = E::pack2(o[j][dt][4 * g4 + 0] * inv, o[j][dt][4 * g4 + 1] * inv);
             const u32 w1 = E::pack2(o[j][dt][4 * g4 + 2] * inv, o[j][dt][4 * g4 + 3] * inv);
-            *(u32x2*)(op + d0) = (u32x2){w0, w1};
+            store4<PARTIAL>(op, d0, a.Dq, w0, w1);
           }
         }
         if (a.score && a.bias && hh == 0) {
@@ -1143,7 +1158,7 @@ __global__ __launch_bounds__((64 * ReplayShape<TPW, DP>::NW), (ReplayShape<TPW, 
     const bool ok = rin && qr < N;
     const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
 #pragma unroll
-    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? (load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.D : DP, a.qvec) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < NDC; ++c) qf[j][c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg) : (u32x4){0u, 0u, 0u, 0u};
     const float br = ok ? a.bias[(long long)(b * a.Hq + head) * N + qr] : POS_INF;
 #pragma unroll
     for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
@@ -1321,16 +1336,21 @@ bool kv_ok(const void* p, const long long* st, int N, int D) {
 
 }  // namespace
 
+bool fast_layout(const AttnArgs& a) {
+  return fast_slot(a.D) >= 0 && kv_ok(a.k, a.ks, a.N, a.D) && kv_ok(a.v, a.vs, a.N, a.D);
+}
+
 bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   const int slot = fast_slot(a.D);
   if (slot < 0) return false;
   // Q is read once per row tile, element-wise when it is not 16-byte vectorisable (any
-  // strides); K and V go through the tile DMA, which needs aligned unit-stride rows. A zero
-  // scale takes the generic kernel.
-  if (!(a.abs_scale_log2 > 0.f)) return false;
-  if (!kv_ok(a.k, a.ks, a.N, a.D) || !kv_ok(a.v, a.vs, a.N, a.D)) return false;
+  // strides); K and V go through the tile DMA, which needs aligned unit-stride rows. The
+  // scale must be positive here: the caller runs a negative one as |scale| on -Q and a zero
+  // one with Q zeroed at load (AttnArgs::qmask).
+  if (!(a.abs_scale_log2 > 0.f) || !fast_layout(a)) return false;
   const bool fused = a.score && !a.bias;
-  const int partial = a.D != 32 * (slot + 1) ? 1 : 0;
+  // below the tile dim (the PARTIAL instantiation) when K/V or Q have fewer channels
+  const int partial = (a.D != 32 * (slot + 1) || a.Dq != 32 * (slot + 1)) ? 1 : 0;
   if (!fused && (slot == 2 || slot == 3) && ((FE_ATTN_RT2 >> slot) & 1) && (!partial || FE_ATTN_RT2_PARTIAL)) {
     plan = g_rt2[2 * (2 * (dtype == 1 ? 1 : 0) + slot - 2) + partial];
     return true;
@@ -1344,7 +1364,7 @@ bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan) {
   FusedPlan fp;
   if (!fast_plan(a, dtype, fp)) return false;
   const int slot = fast_slot(a.D);
-  plan = g_replay[2 * ((dtype == 1 ? kFastDims : 0) + slot) + (a.D != 32 * (slot + 1) ? 1 : 0)];
+  plan = g_replay[2 * ((dtype == 1 ? kFastDims : 0) + slot) + ((a.D != 32 * (slot + 1) || a.Dq != 32 * (slot + 1)) ? 1 : 0)];
   return true;
 }
 

@@ -28,6 +28,8 @@ _SIGNATURES = {
                                   ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_float, _i64, _vp]),
     "fe_prefill_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, ctypes.c_int]),
+    "fe_prefill_workspace_bytes_kv": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, ctypes.c_int, _vp, _I64P,
+                                                        _vp, _I64P]),
     "fe_replay_rows": (_i64, [_i64, _i64, ctypes.c_float]),
     "fe_prefill_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _I64P, _I64P, _I64P,
                                      ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,

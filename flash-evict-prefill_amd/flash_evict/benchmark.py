@@ -25,12 +25,14 @@ Modes (q [1,H,N,D], k/v [1,Hkv,N,D] bf16):
   --kernels    the HBM-bound kernels on scaled synthetics (the headline's score array is
                only 1 MiB, where they are launch-latency bound): achieved GB/s of
                algorithmic bytes (each input byte read once, each output byte written once)
-  --generic    prefill on the shapes and layouts the gfx950 fast path does not take (head
-               dims that are not a multiple of 8, a zero scale, K/V rows off 16-byte
-               alignment), next to the fast path at D = 32, 64, 80, 96, 128, 192 and 256 (and
-               at D = 128 with a negative scale and with a channel-strided q, which it reads
-               element-wise): attention only, and with every row replayed; TFLOP/s of the work
-               the caller asked for (at D = 80 the kernels compute on 96-channel tiles)
+  --generic    prefill on the shapes, scales and layouts the fast kernels do not read in
+               place (head dims that are not a multiple of 8 and K/V rows off 16-byte
+               alignment, which prefill() repacks into its workspace; a zero scale, run with Q
+               zeroed at load), and the first two through the workspace-free entry point (the
+               generic kernel), next to the fast path at D = 32, 64, 80, 96, 128, 192 and 256
+               (and at D = 128 with a negative scale and with a channel-strided q, which it
+               reads element-wise): attention only, and with every row replayed; TFLOP/s of the
+               work the caller asked for (at D = 80 the kernels compute on 96-channel tiles)
 
 Run as `python -m flash_evict.benchmark --lengths 8192 32768 --heads 28 --kv-heads 4
 --dim 128 --output benchmark.json` with flash-evict-prefill_amd/ on PYTHONPATH.
@@ -372,9 +374,31 @@ def _attention_flop(hq, n, d, replay):
     return (4 + (2 if replay else 0)) * pairs * d * hq
 
 
+def _workspace_free(q, k, v, scale, replay):
+    """fe_prefill (no workspace) on q, k, v: the fused kernel, or the generic one where the fast
+    kernels cannot read K/V in place or the scale is zero."""
+    from . import _lib
+    from .prefill import _DTYPES
+    b, h, n, d = q.shape
+    hk = k.shape[1]
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    imp = torch.empty((b, hk, n), dtype=torch.float32, device=q.device)
+    L = _lib.lib()
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr() if replay else None, b, h, hk,
+            n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype],
+            d ** -0.5 if scale is None else scale, 1, 1, int(replay), 0.0, n)
+
+    def fn():
+        _lib.check(L.fe_prefill(*args, torch.cuda.current_stream().cuda_stream), "fe_prefill")
+    return fn
+
+
 @torch.inference_mode()
 def generic_rows(repeats, n=8192, hq=32, hk=8):
-    """prefill() on the layouts of the generic kernel (fe_attn.hip) and of the fast path."""
+    """Attention (and attention with every row replayed) on the layouts and scales the fast
+    kernels do not read in place: through prefill() (repacked K/V, zero scale on the fast
+    kernels) and through the workspace-free entry point (the generic kernel), next to the fast
+    path on ordinary layouts."""
     g = torch.Generator(device="cuda").manual_seed(SEED)
 
     def inputs(d):
@@ -396,25 +420,34 @@ def generic_rows(repeats, n=8192, hq=32, hk=8):
         v = flat[1 + size:1 + 2 * size].view(1, hk, n, d)
         return q, k, v
 
-    cases = [("fast D=128", "fast", 128, lambda: inputs(128), None),
-             ("fast D=64", "fast", 64, lambda: inputs(64), None),
-             ("fast D=96", "fast", 96, lambda: inputs(96), None),
-             ("fast D=32", "fast", 32, lambda: inputs(32), None),
-             ("fast D=80", "fast", 80, lambda: inputs(80), None),
-             ("fast D=192", "fast", 192, lambda: inputs(192), None),
-             ("fast D=256", "fast", 256, lambda: inputs(256), None),
-             ("generic D=100", "generic", 100, lambda: inputs(100), None),
-             ("generic D=256 zero scale", "generic", 256, lambda: inputs(256), 0.0),
-             ("fast D=128 negative scale", "fast", 128, lambda: inputs(128), -(128 ** -0.5)),
-             ("generic D=128 zero scale", "generic", 128, lambda: inputs(128), 0.0),
-             ("fast D=128 q channel stride 2", "fast", 128, lambda: strided_q(128), None),
-             ("generic D=128 K/V rows misaligned", "generic", 128, lambda: offset_kv(128), None)]
+    # path "fast": prefill() on the fast kernels as laid out; "repacked": prefill() copies K/V the
+    # fast kernels cannot read into its workspace first; "zero scale": fast kernels with Q zeroed
+    # at load (with or without a workspace); "generic": the workspace-free entry point fe_prefill,
+    # whose only kernel for these layouts is the generic one (nowhere to repack)
+    cases = [("D=128", "fast", 128, lambda: inputs(128), None),
+             ("D=64", "fast", 64, lambda: inputs(64), None),
+             ("D=96", "fast", 96, lambda: inputs(96), None),
+             ("D=32", "fast", 32, lambda: inputs(32), None),
+             ("D=80", "fast", 80, lambda: inputs(80), None),
+             ("D=192", "fast", 192, lambda: inputs(192), None),
+             ("D=256", "fast", 256, lambda: inputs(256), None),
+             ("D=100", "repacked", 100, lambda: inputs(100), None),
+             ("D=100", "generic", 100, lambda: inputs(100), None),
+             ("D=256 zero scale", "zero scale", 256, lambda: inputs(256), 0.0),
+             ("D=128 negative scale", "fast", 128, lambda: inputs(128), -(128 ** -0.5)),
+             ("D=128 zero scale", "zero scale", 128, lambda: inputs(128), 0.0),
+             ("D=128 q channel stride 2", "fast", 128, lambda: strided_q(128), None),
+             ("D=128 K/V rows misaligned", "repacked", 128, lambda: offset_kv(128), None),
+             ("D=128 K/V rows misaligned", "generic", 128, lambda: offset_kv(128), None)]
     out = []
     for name, path, d, make, scale in cases:
         q, k, v = make()
         for replay in (False, True):
-            fn = (lambda: prefill(q, k, v, scale=scale, recency_decay=0.0)) if replay else \
-                 (lambda: prefill(q, k, v, scale=scale, score=False))
+            if path == "generic":
+                fn = _workspace_free(q, k, v, scale, replay)
+            else:
+                fn = (lambda: prefill(q, k, v, scale=scale, recency_decay=0.0)) if replay else \
+                     (lambda: prefill(q, k, v, scale=scale, score=False))
             # ten warm-ups: the part runs the first launches of a fast-path case at a higher
             # clock than it holds once its power draw has built up
             ms = statistics.median(event_samples(fn, repeats, warmup=10))

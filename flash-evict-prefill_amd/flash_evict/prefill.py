@@ -73,8 +73,10 @@ def prefill(q, k, v, *, causal=True, value_weighted=True, score=True,
     L = _lib.lib()
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        # workspace of the split attention/replay schedule: one float per query row
-        ws_bytes = L.fe_prefill_workspace_bytes(b, h, n, int(bool(score)))
+        # workspace: replay biases (one float per query row), the work-item counters, and
+        # room to repack K/V the fast kernels cannot read in place
+        ws_bytes = L.fe_prefill_workspace_bytes_kv(b, h, hk, n, d, int(bool(score)), k.data_ptr(), _lib.strides(k),
+                                                   v.data_ptr(), _lib.strides(v))
         ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device) if ws_bytes else None
         rc = L.fe_prefill_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                              importance.data_ptr() if score else None,

@@ -92,7 +92,8 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  *     up (the call zeroes them first), instead of one per workgroup index. Each item is
  *     computed the same way whichever workgroup takes it: the output is bitwise that of the
  *     static schedule, the importance equal up to FP32 atomic order;
- *   * score == 0 uses the counters alone.
+ *   * score == 0 uses the counters alone;
+ *   * a zero scale runs on the fast kernels with Q zeroed at load (every logit exactly 0).
  * At head dims 72..128 (multiples of 8) the split schedule's attention kernel holds two row
  * tiles per wave and takes a row's reference max over its first 32 keys instead of 64: the
  * output then agrees with fe_prefill's to within two roundings of the probabilities, the
@@ -102,6 +103,19 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  * interface as fe_prefill.
  */
 size_t fe_prefill_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int score);
+/*
+ * fe_prefill_workspace_bytes plus, when the fast kernels cannot read K or V as laid out (rows
+ * off 16-byte alignment, a channel stride other than 1, broadcast rows, a head dim that is not
+ * a multiple of 8), room for both repacked into aligned rows of D rounded up to 8 channels
+ * (2 * B*Hkv*N*ceil8(D) elements, each area 256-byte aligned). With that much workspace
+ * fe_prefill_ws copies K and V there (an HBM-bound kernel) and runs the fast kernels instead of
+ * the generic one; the output and importance are those of the same call on a contiguous copy.
+ * The pointers are only inspected (alignment), never dereferenced. No counterpart in the
+ * reference, whose Triton kernel reads any strides in place (prefill.py:131-136).
+ */
+size_t fe_prefill_workspace_bytes_kv(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int score,
+                                     const void* k, const int64_t* k_strides, const void* v,
+                                     const int64_t* v_strides);
 int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float* importance,
                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,

@@ -112,3 +112,32 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     finally:
         monkeypatch.delenv("FLASH_EVICT_LIB")
         importlib.reload(_lib)
+
+
+def test_workspace_sizer_adds_repack_room_only_for_layouts_the_fast_kernels_cannot_read():
+    """fe_prefill_workspace_bytes_kv inspects the K/V pointers' alignment and strides (it never
+    dereferences them): aligned unit-stride rows of a head dim that is a multiple of 8 need only the
+    base workspace; misaligned or channel-strided rows, broadcasts and other head dims add room for
+    K and V repacked to D rounded up to 8 channels (256-byte aligned areas)."""
+    L = _lib.lib()
+    B, Hq, Hkv, N = 1, 8, 2, 1000
+
+    def size(d, kptr, kst, vptr=4096, vst=None, score=1):
+        vst = vst or (Hkv * N * d, N * d, d, 1)
+        return L.fe_prefill_workspace_bytes_kv(B, Hq, Hkv, N, d, score, ctypes.c_void_p(kptr),
+                                               (ctypes.c_int64 * 4)(*kst), ctypes.c_void_p(vptr),
+                                               (ctypes.c_int64 * 4)(*vst))
+
+    def repack(d):
+        dp = (d + 7) // 8 * 8
+        return 2 * ((B * Hkv * N * dp * 2 + 255) // 256 * 256)
+
+    for score in (0, 1):
+        base = L.fe_prefill_workspace_bytes(B, Hq, N, score)
+        assert size(128, 4096, (Hkv * N * 128, N * 128, 128, 1), score=score) == base
+        assert size(128, 4098, (Hkv * N * 128, N * 128, 128, 1), score=score) == base + repack(128)
+        assert size(128, 4096, (2 * Hkv * N * 128, 2 * N * 128, 256, 2), score=score) == base + repack(128)
+        assert size(128, 4096, (Hkv * 128, 128, 0, 1), score=score) == base + repack(128)      # broadcast over N
+        assert size(100, 4096, (Hkv * N * 100, N * 100, 100, 1), vst=(Hkv * N * 100, N * 100, 100, 1),
+                    score=score) == base + repack(100)
+        assert size(128, 4096, (Hkv * N * 128, N * 128, 128, 1), vptr=4100, score=score) == base + repack(128)

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import flash_evict
-from flash_evict import prefill
+from flash_evict import _lib, prefill
 from oracle.attention import materialized
 from _helpers import seeded_randn
 
@@ -88,6 +88,86 @@ def test_unusual_layouts():
     ref_out, ref_imp = materialized(q.cpu(), k0.cpu(), k0.cpu())
     torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
     torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+def _misaligned(x):
+    """The same values, 2 bytes off 16-byte alignment (contiguous otherwise)."""
+    flat = torch.zeros(x.numel() + 1, dtype=x.dtype, device=x.device)
+    flat[1:] = x.reshape(-1)
+    return flat[1:].view(x.shape)
+
+
+def _channel_strided(x):
+    """The same values with channel stride 2."""
+    wide = torch.zeros(x.shape[:-1] + (2 * x.shape[-1],), dtype=x.dtype, device=x.device)
+    wide[..., ::2] = x
+    return wide[..., ::2]
+
+
+@pytest.mark.parametrize("d", [64, 128, 192])
+def test_repacked_kv_equals_contiguous_call(d):
+    """K/V the tile DMA cannot read in place (2 bytes off alignment; channel stride 2): prefill()
+    sizes its workspace with fe_prefill_workspace_bytes_kv, the library copies K and V into it
+    and runs the fast kernels, so the output equals the call on the contiguous tensors bit for
+    bit and the importance equals it up to FP32 atomic order."""
+    print("repacked K/V d=%d" % d, flush=True)
+    q, k, v = _qkv(hq=4, hk=2, n=300, d=d, seed=31)
+    for causal in (True, False):
+        ref_out, ref_imp = prefill(q, k, v, causal=causal, recency_decay=0.02)
+        for kk, vv in ((_misaligned(k), _channel_strided(v)), (_channel_strided(k), _misaligned(v))):
+            assert kk.data_ptr() % 16 != 0 or kk.stride(-1) != 1
+            out, imp = prefill(q, kk, vv, causal=causal, recency_decay=0.02)
+            assert torch.equal(out, ref_out)
+            assert float((imp - ref_imp).abs().max()) <= 2e-6 * float(ref_imp.abs().max())
+
+
+@pytest.mark.parametrize("d", [100, 37])
+def test_head_dims_not_multiple_of_8_on_the_fast_path(d):
+    """A head dim that is not a multiple of 8: K and V are repacked to D rounded up to 8 channels
+    (zeros past D), Q is read element-wise up to D and the output stores D channels (one by one
+    when D is not a multiple of 4). Against the FP32 oracle, with and without a causal mask and
+    through the workspace-free entry point (the generic kernel) as well."""
+    print("head dim %d" % d, flush=True)
+    q, k, v = _qkv(hq=4, hk=2, n=200, d=d, seed=33)
+    for causal in (True, False):
+        ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), causal=causal, recency_decay=0.02)
+        out, imp = prefill(q, k, v, causal=causal, recency_decay=0.02)
+        torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+        torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+        assert torch.isfinite(out).all()
+    # the generic kernel (no workspace: nowhere to repack)
+    L = _lib.lib()
+    out = torch.empty_like(q)
+    imp = torch.empty((1, 2, 200), dtype=torch.float32, device=q.device)
+    _lib.check(L.fe_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), 1, 4, 2, 200, d,
+                            _lib.strides(q), _lib.strides(k), _lib.strides(v), 1, d ** -0.5, 1, 1, 1, 0.02, 200,
+                            torch.cuda.current_stream().cuda_stream), "fe_prefill")
+    torch.cuda.synchronize()
+    ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), causal=True, recency_decay=0.02)
+    torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+    torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_zero_scale_fast_and_generic(d):
+    """scale = 0: the fast kernels run it with Q zeroed at load (every logit exactly 0: uniform
+    attention over the visible keys), the workspace-free entry point with the generic kernel.
+    Both against the FP32 oracle."""
+    print("zero scale d=%d" % d, flush=True)
+    q, k, v = _qkv(hq=4, hk=2, n=150, d=d, seed=35)
+    ref_out, ref_imp = materialized(q.cpu(), k.cpu(), v.cpu(), scale=0.0)
+    out, imp = prefill(q, k, v, scale=0.0)
+    torch.testing.assert_close(out.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+    torch.testing.assert_close(imp.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
+    L = _lib.lib()
+    out2 = torch.empty_like(q)
+    imp2 = torch.empty((1, 2, 150), dtype=torch.float32, device=q.device)
+    _lib.check(L.fe_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out2.data_ptr(), imp2.data_ptr(), 1, 4, 2, 150,
+                            d, _lib.strides(q), _lib.strides(k), _lib.strides(v), 1, 0.0, 1, 1, 1, 0.0, 150,
+                            torch.cuda.current_stream().cuda_stream), "fe_prefill")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out2.float().cpu(), ref_out, atol=1.2e-2, rtol=6e-3)
+    torch.testing.assert_close(imp2.cpu(), ref_imp, atol=3e-5, rtol=4e-4)
 
 
 @pytest.mark.parametrize("d", [64, 128])
