@@ -168,8 +168,8 @@ def test_long_131k_planted_keys():
     print("long131k importance element-wise max rel err %.3e" % rel, flush=True)
     _, ref_keep = osel.select_tokens(ref_imp.cpu().numpy(), 1024, reserved_recent=64)
     assert_same_selection(keep, torch.from_numpy(ref_keep), ref_imp.cpu(), 1024, 64, rtol=1e-3)
-    # the output of the first, a middle and the last (planted) query blocks of every head
-    rows = [(0, 1024), (n // 2 - 512, n // 2 + 512), (n - 1024, n)]
-    ref_out, _ = chunked(q, k, v, block=1024, query_rows=rows, value_weighted=False)
-    for r0, r1 in rows:
-        assert (out[:, :, r0:r1].float() - ref_out[:, :, r0:r1]).abs().max() <= 2e-2, (r0, r1)
+    # the output of every row of every head
+    del ref_imp
+    worst = out_err_all_rows(out, q, k, v, block=2048)
+    print("long131k out max-abs-err over all rows: %.4f" % worst, flush=True)
+    assert worst <= 2e-2
