@@ -249,7 +249,7 @@ def main():
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-replay", action="store_true")
-    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "fused_attn_score_headline_traffic.json"),
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "attn_replay_headline_traffic.json"),
                     help="rocprofv3 PMC summary giving HBM bytes per fused launch (optional)")
     args = ap.parse_args()
 

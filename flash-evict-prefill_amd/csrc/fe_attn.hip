@@ -658,6 +658,12 @@ namespace fe {
 // column; the replay's own term exp2(s*scale*log2e - b_q) is bounded by
 // 2^(-decay*log2e*t) <= 2^-151.4 there and underflows to 0 as well. Rows with t < 105/decay
 // are kept: ceil(105/decay) of them, or all `window` rows when that is fewer.
+// Build option: -D FE_DYNAMIC_SCHEDULE=0 keeps the static schedule (item = workgroup index) even
+// with the whole workspace (for A/B measurements).
+#ifndef FE_DYNAMIC_SCHEDULE
+#define FE_DYNAMIC_SCHEDULE 1
+#endif
+
 // Workgroups launched for `items` work items of a kernel that runs one item per workgroup
 // under the dynamic schedule (the replay kernel): one eighth more, rounded up to the 8 XCDs
 // the hardware deals workgroups over in turn, so that an XCD that runs faster than the others
@@ -789,7 +795,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // Dynamic schedule (fast attention-only kernels, and the replay kernel): needs the
   // counters, i.e. the whole workspace of fe_prefill_workspace_bytes.
   int* ctr = nullptr;
-  if (fast && (split || !score) && workspace && workspace_bytes >= ws_ctr + kQueueBytes)
+  if (FE_DYNAMIC_SCHEDULE && fast && (split || !score) && workspace && workspace_bytes >= ws_ctr + kQueueBytes)
     ctr = (int*)((char*)workspace + ws_ctr);
   // Workgroups are sized by the plan's row tiles per workgroup.
   a.wg_bh = (int)((tiles_bh + plan.rows - 1) / plan.rows);
