@@ -213,17 +213,35 @@ def cpu_baseline(q, k, v, kw, executed_flop, sample_heads=8):
     }
 
 
-def _timed_layers(step, steps, warmup, tag):
-    """Run `warmup` untimed and `steps` timed layers; return (ms per layer, fused-kernel ms
-    per launch, launches) with the fused kernels timed by the library's HIP events."""
+def _timed_layers(step, steps, warmup, tag, warmup_ms=0.0):
+    """Run at least `warmup` untimed layers, continuing back to back until `warmup_ms` of
+    warm-up have passed, then `steps` timed layers; return (ms per layer, fused-kernel ms per
+    launch, launches, warm-up layers run) with the fused kernels timed by the library's HIP
+    events.
+
+    The minimum warm-up time is there for the GPU's power management: after a change of load
+    the part first runs these kernels at a clock well below the one it then holds (measured on
+    the llama8k layer: about 1.85 GHz for the first layers, 1.55-1.65 GHz from the third to
+    the tenth, 1.93 GHz steady from about the sixtieth layer, 35 ms in), so a few warm-up
+    layers time the controller's transient instead of the kernels."""
     import ctypes
     import torch
     from flash_evict import _lib
     L = _lib.lib()
+    t_start = time.perf_counter()
     for i in range(warmup):
         step()
         torch.cuda.synchronize()
         log("%s warmup %d/%d done" % (tag, i + 1, warmup))
+    done, t_log = warmup, time.perf_counter()
+    while (time.perf_counter() - t_start) * 1e3 < warmup_ms:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
+        done += 8
+        if time.perf_counter() - t_log > 0.5:
+            t_log = time.perf_counter()
+            log("%s warmup: %d layers, %.2f s" % (tag, done, t_log - t_start))
     _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
     _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
     torch.cuda.synchronize()
@@ -237,8 +255,9 @@ def _timed_layers(step, steps, warmup, tag):
     fused_ms = ctypes.c_double(0.0)
     _lib.check(L.fe_fused_timing_read(ctypes.byref(launches), ctypes.byref(fused_ms)), "fe_fused_timing_read")
     ms = elapsed * 1e3 / steps
-    log("%s timed %d steps: %.3f ms/layer" % (tag, steps, ms))
-    return ms, fused_ms.value / max(1, launches.value), launches.value
+    log("%s timed %d steps after %d warm-up layers (%.2f s): %.3f ms/layer" % (
+        tag, steps, done, t0 - t_start, ms))
+    return ms, fused_ms.value / max(1, launches.value), launches.value, done
 
 
 def main():
@@ -246,6 +265,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup-ms", type=float, default=1500.0,
+                    help="minimum warm-up time per measured phase (untimed layers run back to back)")
     ap.add_argument("--config", default="headline", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-full-replay", action="store_true")
@@ -284,19 +305,20 @@ def main():
         return algorithmic_flop(b, hq, n, d, kw["observation_window"], decay, causal=causal, effective=effective)
 
     with torch.inference_mode():
-        ms, fused_avg_ms, launches = _timed_layers(make_step(kw["recency_decay"]), args.steps, args.warmup,
-                                                   args.config)
+        ms, fused_avg_ms, launches, warm_run = _timed_layers(make_step(kw["recency_decay"]), args.steps,
+                                                             args.warmup, args.config, args.warmup_ms)
         full = None
         if kw["recency_decay"] > 0 and not args.no_full_replay:
             fsteps = max(3, args.steps // 2)
-            f_ms, f_fused, f_launches = _timed_layers(make_step(0.0), fsteps, min(2, args.warmup), "full-replay")
+            f_ms, f_fused, f_launches, f_warm = _timed_layers(make_step(0.0), fsteps, min(2, args.warmup),
+                                                              "full-replay", args.warmup_ms)
             f_flop = flops(0.0)
             f_ach = f_flop / (f_fused * 1e-3) / 1e12
             full = {"recency_decay": 0.0, "replay_rows": replay_rows(n, kw["observation_window"], 0.0),
                     "executed_tflop": round(f_flop / 1e12, 4), "ms_per_layer": round(f_ms, 4),
                     "fused_mean_ms": round(f_fused, 4), "fused_achieved_tflops": round(f_ach, 2),
                     "fused_frac": round(f_ach / PEAK_BF16_TFLOPS, 4), "launches": f_launches,
-                    "steps": fsteps}
+                    "steps": fsteps, "warmup_layers_run": f_warm}
     flop = flops(kw["recency_decay"], effective=False)
     executed = flops(kw["recency_decay"])
     achieved = executed / (fused_avg_ms * 1e-3) / 1e12
@@ -317,6 +339,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_layers_run": warm_run,
+        "warmup_min_ms": args.warmup_ms,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
