@@ -33,13 +33,15 @@ struct AttnArgs {
   int* queue;                       // dynamic schedule: item counter, zero at launch (else null)
   int nitems;                       // dynamic schedule: work items of the launch
   int nstatic;                      // dynamic schedule: workgroups launched (each starts with item blockIdx.x)
+  int tail;                         // dynamic schedule: first item of the queues' light parts (nitems: none)
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
 };
 
 // Work-item counters of the dynamic schedule, at the end of the prefill workspace (the
 // next 256-byte boundary after the replay biases): eight per kernel (one per XCD queue), each
 // on its own 128-byte line, the attention kernel's from word 0 and the replay kernel's from
-// word kQueueReplay. Zeroed before every launch.
+// word kQueueReplay; a queue's counters are the 64-bit words at ints 0 and 2 of its line (its
+// heavy and light parts, take_item in fe_attn_fast.hip). Zeroed before every launch.
 constexpr int kQueueStride = 32;
 constexpr int kQueueReplay = 8 * kQueueStride;
 constexpr int kQueueWords = 2 * kQueueReplay;

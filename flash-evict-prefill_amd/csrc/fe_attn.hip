@@ -671,6 +671,42 @@ namespace fe {
 // once.
 int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64_t)7); }
 
+// Shares of a launch's work in the light parts of the dynamic schedule's queues (take_item in
+// fe_attn_fast.hip): the lightest items, which other XCDs take before any heavy one once their
+// own queues are empty, so that the XCDs' different speeds (several percent under these
+// kernels) even out on small items at the end. Build options, for measurement.
+#ifndef FE_TAIL_ATTN
+#define FE_TAIL_ATTN 0.2
+#endif
+#ifndef FE_TAIL_REPLAY
+#define FE_TAIL_REPLAY 0.0
+#endif
+
+// Key tiles of the query rows of row tiles [.., t_end) of one (batch, KV head): causal rows see
+// keys up to their own position.
+int64_t item_key_tiles(int64_t t_end, int64_t G, int64_t N, bool causal) {
+  const int64_t q_hi = ((t_end - 1) / G + 1) * 32;
+  const int64_t kv_end = causal ? (q_hi < N ? q_hi : N) : N;
+  return (kv_end + 63) / 64;
+}
+
+// First item of the queues' light parts. Items are numbered heaviest first in groups of BH (one
+// per (batch, KV head), equal work within a group); the tail is the lightest groups holding at
+// most `share` of the launch's work (work(g): of group g, in key tiles, plus two tiles of fixed
+// cost per item), never starting below nstatic.
+template <typename W>
+int64_t tail_start(int64_t ngroups, int64_t BH, int64_t nstatic, double share, W work) {
+  const int64_t nitems = ngroups * BH;
+  if (!(share > 0.0)) return nitems;
+  double total = 0.0;
+  for (int64_t g = 0; g < ngroups; ++g) total += (double)(work(g) + 2);
+  double acc = 0.0;
+  int64_t g = ngroups;
+  while (g > 0 && acc + (double)(work(g - 1) + 2) <= share * total) acc += (double)(work(--g) + 2);
+  const int64_t t = g * BH;
+  return t < nstatic ? nstatic : t;
+}
+
 int64_t replay_rows(int64_t N, int64_t window, float recency_decay) {
   if (!(recency_decay > 0.f)) return window;
   const double span = ceil(105.0 / (double)recency_decay);
@@ -727,6 +763,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.queue = nullptr;
   a.nitems = 0;
   a.nstatic = 0;
+  a.tail = 0;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -817,6 +854,12 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     a.queue = ctr;
     a.nitems = (int)items;
     a.nstatic = (int)(items < resident ? items : resident);
+    const int64_t rows = plan.rows, wgb = a.wg_bh;
+    a.tail = (int)tail_start(wgb, B * Hkv, a.nstatic, FE_TAIL_ATTN, [&](int64_t g) {
+      const int64_t wg = wgb - 1 - g;
+      const int64_t t_end = (wg + 1) * rows < tiles_bh ? (wg + 1) * rows : tiles_bh;
+      return item_key_tiles(t_end, G, N, causal != 0);
+    });
     grid = a.nstatic;
   }
   if (score || ctr) {
@@ -881,6 +924,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       r.queue = ctr + kQueueReplay;
       r.nitems = (int)rgrid;
       r.nstatic = (int)(rgrid < resident ? rgrid : resident);
+      const int64_t rrows = rplan.rows, rwgb = r.wg_bh;
+      r.tail = (int)tail_start(rgrid / (B * Hkv), B * Hkv, r.nstatic, FE_TAIL_REPLAY, [&](int64_t g) {
+        const int64_t ks = g % rs, wg = rwgb - 1 - g / rs;
+        const int64_t t_end = (wg + 1) * rrows < tiles_bh ? (wg + 1) * rrows : tiles_bh;
+        const int64_t all = item_key_tiles(t_end, G, N, causal != 0), per = (all + rs - 1) / rs;
+        const int64_t lo = ks * per, hi = lo + per < all ? lo + per : all;
+        return hi > lo ? hi - lo : (int64_t)0;
+      });
       rgrid = one_shot_grid(rgrid);
     }
     void* rargs[] = {&r};

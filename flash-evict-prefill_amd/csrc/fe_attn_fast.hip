@@ -149,51 +149,92 @@ __device__ __forceinline__ int lane_now() {
 // items. Items are numbered heaviest first, with consecutive numbers on different KV heads,
 // and the rest are dealt to eight queues, one per XCD: queue x holds items x, x + 8, x + 16,
 // ... past the first ones (with B*Hkv a multiple of 8, the KV heads h with h % 8 == x, whose
-// K/V tiles that XCD's L2 then serves). A workgroup takes its next item from its own XCD's
-// queue (hardware register XCC_ID) or, once that is empty, from the next queue with items
-// left, and exits when none has any. So each item goes to whichever CU frees up first within
-// its XCD, without waiting for the hardware dispatcher, which starts workgroups in order and
-// holds a free CU of one XCD until the next workgroup for another XCD has found room; and
+// K/V tiles that XCD's L2 then serves), heaviest first, in two parts: the heavy items below
+// a.tail and the light ones from a.tail on (the last groups of items, holding a fixed share of
+// the work, chosen by the host). A workgroup on XCD x (hardware register XCC_ID) takes the
+// front of its own heavy part, then its own light part, then the light part of the nearest
+// other queue with light items left, and only then the back of another queue's heavy part;
+// it exits when every queue is empty. So each item goes to whichever CU frees up first within
+// its XCD, without waiting for the hardware dispatcher (which starts workgroups in order and
+// holds a free CU of one XCD until the next workgroup for another XCD has found room), and
 // XCDs that run faster than the others (their clocks differ by several percent under these
-// kernels) take over the lightest items of the slower ones. The barrier before the fetch
-// orders every wave's LDS reads of the previous item (and its read of the shared index)
-// before the next item's first tile DMA and the next index. Returns a block-uniform index.
-// wv is the wave's index in the workgroup (uniform); the lane index is taken opaquely, so
-// nothing lane-derived is hoisted out of the caller's item loop and held across it.
+// kernels) help the slower ones with light items: stealing heavy items instead, the fast XCDs
+// ran dry while a slow XCD still held items of hundreds of microseconds, and the kernel ended
+// up to 240 us after its first CUs went idle at the headline shape. The barrier before the
+// fetch orders every wave's LDS reads of the previous item (and its read of the shared index)
+// before the next item's first tile DMA and the next index. Returns a block-uniform index. wv
+// is the wave's index in the workgroup (uniform); the lane index is taken opaquely, so nothing
+// lane-derived is hoisted out of the caller's item loop and held across it.
 __device__ __forceinline__ int queue_len(int nitems, int x) { return (nitems - x + 7) >> 3; }
 
+// Counters of queue x, on its own 128-byte line: the heavy part's 64-bit word (items taken
+// from its front in the low half, by the queue's own XCD, and from its back in the high half,
+// by other XCDs) and the light part's word (items taken, by anyone). Every take adds one to one
+// half in one atomic, so the takes of a part are totally ordered. A heavy take succeeds iff
+// front + back < n (the part's items) before it, so the successful front takes are positions
+// 0 .. F-1 and the back takes n-1 .. n-B with F + B <= n; a light take succeeds iff its
+// counter was below the part's length. Every item is taken exactly once, and a failed take
+// leaves that part exhausted for good.
+__device__ __forceinline__ unsigned long long* heavy_word(const AttnArgs& a, int x) {
+  return (unsigned long long*)(a.queue + kQueueStride * x);
+}
+__device__ __forceinline__ unsigned long long* light_word(const AttnArgs& a, int x) {
+  return (unsigned long long*)(a.queue + kQueueStride * x + 2);
+}
+
 // The next item for a workgroup on XCD x, taken by wave 0 (uniform result; a.nitems when
-// every queue is empty).
+// every queue is empty). Queue q's heavy items are positions [queue_len(nstatic, q),
+// queue_len(tail, q)) and its light items [queue_len(tail, q), queue_len(nitems, q)); item =
+// 8 * position + q.
 __device__ __forceinline__ int take_item(const AttnArgs& a) {
   const int lane = lane_now();
   const int x = (int)(__builtin_amdgcn_s_getreg(kHwRegXccId) & 7u);
-  // the j-th item taken from queue q is its entry queue_len(nstatic, q) + j
   int got = -1;
   if (lane == 0) {
-    const int j = queue_len(a.nstatic, x) + atomicAdd(a.queue + kQueueStride * x, 1);
-    if (j < queue_len(a.nitems, x)) got = 8 * j + x;
+    const int p0 = queue_len(a.nstatic, x), pt = queue_len(a.tail, x), n = pt - p0;
+    const unsigned long long w = atomicAdd(heavy_word(a, x), 1ull);
+    if ((int)(unsigned)w + (int)(w >> 32) < n) {
+      got = 8 * (p0 + (int)(unsigned)w) + x;
+    } else {
+      const int j = (int)atomicAdd(light_word(a, x), 1ull);
+      if (j < queue_len(a.nitems, x) - pt) got = 8 * (pt + j) + x;
+    }
   }
   int item = __shfl(got, 0);
   // Other queues, nearest first: lanes 0-6 read queues x+1 .. x+7 at once, lane 0 takes from
-  // the first with items left. Each failed take leaves that queue exhausted for good (the
-  // counters only grow), so at most seven rounds run.
-  for (int round = 0; round < 7 && item < 0; ++round) {
-    bool left = false;
-    if (lane < 7) {
-      const int qx = (x + 1 + lane) & 7;
-      left = queue_len(a.nstatic, qx) +
-                 __hip_atomic_load(a.queue + kQueueStride * qx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             queue_len(a.nitems, qx);
+  // the first with items left (light parts, then heavy ones). Each failed take leaves that
+  // part exhausted for good, so at most seven rounds of each kind run.
+  for (int heavy = 0; heavy < 2 && item < 0; ++heavy) {
+    for (int round = 0; round < 7 && item < 0; ++round) {
+      bool left = false;
+      if (lane < 7) {
+        const int qx = (x + 1 + lane) & 7;
+        const int p0 = queue_len(a.nstatic, qx), pt = queue_len(a.tail, qx);
+        if (heavy) {
+          const unsigned long long w = __hip_atomic_load(heavy_word(a, qx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          left = (int)(unsigned)w + (int)(w >> 32) < pt - p0;
+        } else {
+          const unsigned long long w = __hip_atomic_load(light_word(a, qx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          left = (int)w < queue_len(a.nitems, qx) - pt;
+        }
+      }
+      const unsigned long long m = __ballot(left);
+      if (m == 0) break;
+      const int qx = (x + __ffsll(m)) & 7;
+      got = -1;
+      if (lane == 0) {
+        const int p0 = queue_len(a.nstatic, qx), pt = queue_len(a.tail, qx);
+        if (heavy) {
+          const unsigned long long w = atomicAdd(heavy_word(a, qx), 1ull << 32);
+          const int bk = (int)(w >> 32);
+          if ((int)(unsigned)w + bk < pt - p0) got = 8 * (pt - 1 - bk) + qx;
+        } else {
+          const int j = (int)atomicAdd(light_word(a, qx), 1ull);
+          if (j < queue_len(a.nitems, qx) - pt) got = 8 * (pt + j) + qx;
+        }
+      }
+      item = __shfl(got, 0);
     }
-    const unsigned long long m = __ballot(left);
-    if (m == 0) break;
-    const int qx = (x + __ffsll(m)) & 7;
-    got = -1;
-    if (lane == 0) {
-      const int j = queue_len(a.nstatic, qx) + atomicAdd(a.queue + kQueueStride * qx, 1);
-      if (j < queue_len(a.nitems, qx)) got = 8 * j + qx;
-    }
-    item = __shfl(got, 0);
   }
   return item < 0 ? a.nitems : item;
 }

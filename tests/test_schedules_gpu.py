@@ -60,6 +60,9 @@ CASES = [
     (1, 28, 4, 3000, 128, torch.bfloat16, True, True, 0.0, 128, "contiguous"),
     (1, 4, 4, 777, 128, torch.bfloat16, False, True, 0.05, 300, "transposed"),
     (1, 8, 1, 65, 64, torch.float16, True, True, 0.0, 1, "contiguous"),
+    # more work items than resident workgroups: the queues' heavy and light parts and stealing
+    # (attention 1024 items, replay 2048 with every row replayed)
+    (1, 32, 8, 16384, 128, torch.bfloat16, True, True, 0.0, 0, "contiguous"),
 ]
 
 
