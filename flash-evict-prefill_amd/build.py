@@ -21,7 +21,7 @@ LIB_NAME = "libflash_evict_hip.so"
 BUILD_DIR = os.path.join(os.path.dirname(HERE), "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_SOURCES = ["fe_attn.hip", "fe_attn_fast.hip", "fe_select.hip", "fe_gather.hip", "fe_snap.hip"]
+HIP_SOURCES = ["fe_attn.hip", "fe_attn_fast.hip", "fe_select.hip", "fe_gather.hip", "fe_snap.hip", "fe_static.hip"]
 CXX_SOURCES = ["fe_api.cpp"]
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in device code (the host pass warns that it

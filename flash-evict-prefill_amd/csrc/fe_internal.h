@@ -20,6 +20,9 @@ void append_select_resources(std::string& out);
 void append_gather_resources(std::string& out);
 void append_snap_resources(std::string& out);
 
+// Device address of fe_prefill_static's workspace on the device of `stream` (fe_static.hip).
+hipError_t static_scratch(hipStream_t stream, float** out);
+
 // Fused-kernel timing (enabled through fe_fused_timing_enable).
 bool fused_timing_enabled();
 void fused_timing_push(hipEvent_t start, hipEvent_t stop);

@@ -130,7 +130,8 @@ int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float*
  * counterpart in the reference; it is for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * The buffer holds FE_STATIC_BIAS_ROWS floats and the work-item counters (16 MiB + 2 KiB) on
- * every GPU the library runs on, kept until the process ends. A scoring call needs
+ * every GPU this entry point has run on, from its first call there until the process ends
+ * (processes that never call it do not hold the buffer). A scoring call needs
  * B*Hq*N <= FE_STATIC_BIAS_ROWS and otherwise fails with FE_ERR_WORKSPACE before launching
  * anything. Every call on one GPU shares that GPU's buffer: calls that overlap on one GPU
  * (concurrent streams or threads) race, so the caller must order them. Results: those of

@@ -144,3 +144,51 @@ def test_static_entry_rejects_sizes_beyond_its_buffer():
         assert rc == FE_ERR_WORKSPACE, (b, hq, n, rc)
         msg = L.fe_last_error().decode()
         assert "static replay-bias buffer" in msg and str(R) in msg, msg
+
+
+_RESERVE_SCRIPT = r"""
+import sys
+sys.path[:0] = sys.argv[1:]
+import torch, flash_evict
+from flash_evict import _lib
+from flash_evict.prefill import _DTYPES
+dev = torch.device("cuda", 0)
+g = torch.Generator(device=dev).manual_seed(5)
+q = torch.randn((1, 8, 1024, 128), device=dev, generator=g).to(torch.bfloat16)
+k = torch.randn((1, 2, 1024, 128), device=dev, generator=g).to(torch.bfloat16)
+v = torch.randn((1, 2, 1024, 128), device=dev, generator=g).to(torch.bfloat16)
+for _ in range(2):
+    out, imp = flash_evict.prefill(q, k, v)
+torch.cuda.synchronize()
+torch.cuda.empty_cache()
+free_after_ws = torch.cuda.mem_get_info()[0]
+L = _lib.lib()
+st = _lib.strides
+rc = L.fe_prefill_static(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr(), 1, 8, 2, 1024,
+                         128, st(q), st(k), st(v), _DTYPES[q.dtype], 128 ** -0.5, 1, 1, 1, 0.0, 1024,
+                         torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+torch.cuda.empty_cache()
+free_after_static = torch.cuda.mem_get_info()[0]
+print("RESERVED_BY_STATIC", rc, free_after_ws - free_after_static)
+"""
+
+
+@pytest.mark.gpu
+def test_static_buffer_reserved_only_by_static_entry():
+    """The static workspace (16 MiB + 2 KiB per GPU) lives in a code object of its own: a process
+    holds it only once it calls fe_prefill_static, not from its first prefill() call. Checked in a
+    fresh process (device free memory after prefill() calls, then after one static call)."""
+    import os
+    import subprocess
+    import sys
+    print("static buffer reservation: fresh process, prefill() twice, then fe_prefill_static once", flush=True)
+    here = os.path.dirname(os.path.abspath(__file__))
+    paths = [os.path.join(os.path.dirname(here), "flash-evict-prefill_amd"), os.path.dirname(here)]
+    res = subprocess.run([sys.executable, "-c", _RESERVE_SCRIPT] + paths, capture_output=True, text=True,
+                         timeout=110)
+    line = [x for x in res.stdout.splitlines() if x.startswith("RESERVED_BY_STATIC")]
+    assert res.returncode == 0 and line, res.stdout + res.stderr
+    _, rc, delta = line[0].split()
+    assert int(rc) == 0
+    assert int(delta) >= 16 * 2**20, "fe_prefill_static reserved %d bytes: its buffer was already held" % int(delta)
