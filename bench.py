@@ -73,14 +73,14 @@ for _n in (8192, 32768, 131072):
                                                       observation_window=0, pool_kernel=1))
 
 
-def kernel_names(cfg):
-    """The attention and replay kernels the split schedule runs for a config (fast layouts):
-    the two-row-tile attention kernel at tile dims 96 and 128, else the one-row-tile one."""
-    e = cfg["dtype"]
-    dp = -(-cfg["D"] // 32) * 32
-    part = "" if dp == cfg["D"] else ",partial"
-    attn = "attn_rt2" if dp in (96, 128) else "attn_fast"
-    return "%s<%s,%d%s>" % (attn, e, dp, part), "replay_fast<%s,%d%s>" % (e, dp, part)
+def last_plan():
+    """Kernels of this thread's last prefill launch, as the library names them (fe_last_plan):
+    the attention kernel, and the replay kernel when the split schedule ran."""
+    import ctypes
+    from flash_evict import _lib
+    buf = ctypes.create_string_buffer(512)
+    _lib.check(_lib.lib().fe_last_plan(buf, len(buf)), "fe_last_plan")
+    return buf.value.decode()
 
 
 def make_inputs(cfg, dev):
@@ -307,6 +307,7 @@ def main():
     with torch.inference_mode():
         ms, fused_avg_ms, launches, warm_run = _timed_layers(make_step(kw["recency_decay"]), args.steps,
                                                              args.warmup, args.config, args.warmup_ms)
+        plan_name = last_plan()
         full = None
         if kw["recency_decay"] > 0 and not args.no_full_replay:
             fsteps = max(3, args.steps // 2)
@@ -331,7 +332,6 @@ def main():
                 traffic = tj.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
-    attn_name, replay_name = kernel_names(cfg)
     record = {
         "metric": "ms/layer + fused attn+score TFLOP/s (% MFMA peak), N=32K Hq32/Hkv8 D128 bf16",
         "value": round(executed / (ms * 1e-3) / 1e12, 2),
@@ -357,7 +357,7 @@ def main():
                    "replay_rows": replay_rows(n, kw["observation_window"], kw["recency_decay"]),
                    "executed_tflop": round(executed / 1e12, 4)},
         "value_defined_work": round(flop / (ms * 1e-3) / 1e12, 2),
-        "roofline": {"bound": "mfma", "kernel": "%s + %s" % (attn_name, replay_name),
+        "roofline": {"bound": "mfma", "kernel": plan_name,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "mean_ms": round(fused_avg_ms, 4), "launches": launches},

@@ -89,6 +89,8 @@ struct ReplayPlan {
   int rows;
   const char* name;
 };
+// The small-grid attention kernel at tile dims 32 and 64 (4-wave workgroups), where it applies.
+bool fast_plan_small(const AttnArgs& a, int dtype, FusedPlan& plan);
 bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan);
 hipError_t prepare_plan(const FusedPlan& plan);
 void append_fast_resources(std::string& out);

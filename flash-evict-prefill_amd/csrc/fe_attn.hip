@@ -33,6 +33,7 @@
 //     different KV heads (the hardware deals blocks round-robin over the 8 XCDs, so each
 //     XCD's L2 sees a small set of KV heads).
 #include <math.h>
+#include <string.h>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -682,6 +683,12 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #define FE_TAIL_REPLAY 0.0
 #endif
 
+// Rounds of resident workgroups up to which tile dims 32 and 64 run the small-grid attention
+// kernel (fast_plan_small). Build option, for measurement.
+#ifndef FE_SMALL_GRID_ROUNDS
+#define FE_SMALL_GRID_ROUNDS 2
+#endif
+
 // Key tiles of the query rows of row tiles [.., t_end) of one (batch, KV head): causal rows see
 // keys up to their own position.
 int64_t item_key_tiles(int64_t t_end, int64_t G, int64_t N, bool causal) {
@@ -712,6 +719,9 @@ int64_t replay_rows(int64_t N, int64_t window, float recency_decay) {
   const double span = ceil(105.0 / (double)recency_decay);
   return span < (double)window ? (int64_t)span : window;
 }
+
+// Kernels of the calling thread's last prefill launch (fe_last_plan).
+thread_local std::string g_last_plan;
 
 static int prefill_impl(const void* q, const void* k, const void* v, void* out, float* importance, int64_t B,
                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D, const int64_t* q_strides,
@@ -829,6 +839,17 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     const FusedEntry& ent = fused_table()[(dtype == FE_DTYPE_BF16 ? kNumDP : 0) + dpi];
     plan = FusedPlan{(const void*)ent.fn, ent.lds, 4, 4, ent.name};
   }
+  hipStream_t stream = (hipStream_t)hip_stream;
+  // Small grids at tile dims 32 and 64: where the 8-wave attention kernel's work items would
+  // fill at most FE_SMALL_GRID_ROUNDS rounds of its resident workgroups, the 4-wave kernel
+  // (twice the items, four workgroups per CU) fills the chip better.
+  FusedPlan small;
+  if (fast && plan.rows == 8 && fast_plan_small(a, dtype, small)) {
+    int64_t res8 = 0;
+    if (resident_blocks(plan.fn, 64 * plan.waves, plan.lds, stream, &res8) == hipSuccess &&
+        B * Hkv * ((tiles_bh + 7) / 8) <= (int64_t)FE_SMALL_GRID_ROUNDS * res8)
+      plan = small;
+  }
   // Dynamic schedule (fast attention-only kernels, and the replay kernel): needs the
   // counters, i.e. the whole workspace of fe_prefill_workspace_bytes.
   int* ctr = nullptr;
@@ -839,7 +860,6 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   const int64_t items = B * Hkv * (int64_t)a.wg_bh;
   int64_t grid = items;
 
-  hipStream_t stream = (hipStream_t)hip_stream;
   hipError_t err = prepare_plan(plan);
   if (err != hipSuccess) {
     set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
@@ -895,6 +915,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       return FE_ERR_HIP;
     }
   }
+  g_last_plan = split ? std::string(plan.name) + " + " + rplan.name : std::string(plan.name);
   void* kargs[] = {&a};
   err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
   if (err != hipSuccess) {
@@ -980,6 +1001,17 @@ extern "C" int fe_prefill(const void* q, const void* k, const void* v, void* out
   clear_error();
   return prefill_impl(q, k, v, out, importance, B, Hq, Hkv, N, D, q_strides, k_strides, v_strides, dtype, scale,
                       causal, value_weighted, score, recency_decay, window, nullptr, 0, hip_stream);
+}
+
+extern "C" int fe_last_plan(char* buf, size_t cap) {
+  clear_error();
+  const std::string& s = fe::g_last_plan;
+  if (!buf || cap < s.size() + 1) {
+    set_error("fe_last_plan: buffer too small; need " + std::to_string(s.size() + 1) + " bytes");
+    return FE_ERR_INVALID;
+  }
+  memcpy(buf, s.c_str(), s.size() + 1);
+  return FE_OK;
 }
 
 extern "C" int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay) {

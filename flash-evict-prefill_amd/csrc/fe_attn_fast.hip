@@ -269,21 +269,25 @@ __device__ __forceinline__ int block_item(const AttnArgs& a, int* s_item, int wv
 // reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
 // Waves per SIMD the fused_fast_kernel instantiation is built for: 12-wave workgroups three,
-// 8-wave ones two, 4-wave ones (tile dim 256: 128 accumulator and 64 Q registers per wave) one.
-template <int NW>
+// 8-wave ones two, 4-wave ones one above tile dim 64 (tile dim 256: 128 accumulator and 64 Q
+// registers per wave) and four at tile dims 32 and 64 (the small-grid kernel: four workgroups
+// per CU, one wave of each per SIMD).
+template <int NW, int DP>
 struct FastOccupancy {
-  static constexpr int WAVES_PER_EU = NW > 8 ? 3 : (NW > 4 ? 2 : 1);
+  static constexpr bool SMALL_GRID = NW == 4 && DP <= 64;
+  static constexpr int WAVES_PER_EU = NW > 8 ? 3 : (NW > 4 ? 2 : (SMALL_GRID ? 4 : 1));
 };
 
 template <typename E, int DP, int NW, bool FUSED, bool PARTIAL>
-__global__ __launch_bounds__(NW * 64, FastOccupancy<NW>::WAVES_PER_EU) void fused_fast_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) void fused_fast_kernel(const AttnArgs a) {
   typedef FastTile<DP> T;
   constexpr int BN = T::BN, NDC = T::NDC, NDT = T::NDT, TILE = T::TILE;
   constexpr int DPW = T::DMA_PER_WAVE;
   constexpr int KH = (NW > 8 || DP > 128) ? 2 : 1;   // K fragment reads per 32-key half
   // 64-key tiles per LDS buffer: two up to tile dim 128 (one barrier per pair of tiles), one
-  // above it, where two double-buffered pairs of K and V tiles would not fit the LDS
-  constexpr int SLOTS = DP <= 128 ? 2 : 1;
+  // above it, where two double-buffered pairs of K and V tiles would not fit the LDS, and in
+  // the small-grid kernel (32 KiB of LDS per workgroup at tile dim 64: four per CU)
+  constexpr int SLOTS = (DP <= 128 && !FastOccupancy<NW, DP>::SMALL_GRID) ? 2 : 1;
   static_assert(NDC % KH == 0, "K fragment groups");
   static_assert(NW % 2 == 0 && NW >= 4, "row tiles per workgroup");
   constexpr float NEG_INF = -__builtin_huge_valf();
@@ -1346,6 +1350,17 @@ FusedPlan fast_entry(const char* name) {
       FE_FAST_DIM(E, e, 160, 8), FE_FAST_DIM(E, e, 192, 8), FE_FAST_DIM(E, e, 224, 4), FE_FAST_DIM(E, e, 256, 4)
 // [dtype][tile dim][partial][fused]
 FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")};
+// Small grids at tile dims 32 and 64 (attention only): 4-wave workgroups of one row tile per
+// wave, single-tile LDS buffers, four workgroups per CU, so twice the work items of the 8-wave
+// kernel and each SIMD's four waves from four workgroups. Chosen by the launch when the 8-wave
+// kernel's items would fill at most a few rounds of its resident workgroups: the reference
+// harness's Hq4/Hkv2 shape at 8K and 32K measured 11% and 4.4% faster, a grid of eight rounds
+// (B1 Hq32/Hkv8 N32768) 3% slower.
+#define FE_FAST_SMALL_DIM(E, e, DP) \
+  fast_entry<E, DP, 4, false, false>("attn_fast4<" e "," #DP ">"), fast_entry<E, DP, 4, false, true>("attn_fast4<" e "," #DP ",partial>")
+// [dtype][tile dim 32, 64][partial]
+FusedPlan g_fast_small[] = {FE_FAST_SMALL_DIM(F16, "f16", 32), FE_FAST_SMALL_DIM(F16, "f16", 64),
+                            FE_FAST_SMALL_DIM(BF16, "bf16", 32), FE_FAST_SMALL_DIM(BF16, "bf16", 64)};
 // Attention-only traversal with two row tiles per wave at tile dims 96 and 128 (attn_rt2_kernel:
 // 8 waves, 16 row tiles per workgroup), head dims below the tile dim included: 3-5% faster than
 // fused_fast_kernel's 12 waves of one row tile on every measured configuration at D = 128, 3% at
@@ -1401,6 +1416,14 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
   return true;
 }
 
+bool fast_plan_small(const AttnArgs& a, int dtype, FusedPlan& plan) {
+  const int slot = fast_slot(a.D);
+  if (slot < 0 || slot > 1 || !(a.abs_scale_log2 > 0.f) || !fast_layout(a) || (a.score && !a.bias)) return false;
+  const int partial = (a.D != 32 * (slot + 1) || a.Dq != 32 * (slot + 1)) ? 1 : 0;
+  plan = g_fast_small[2 * (2 * (dtype == 1 ? 1 : 0) + slot) + partial];
+  return true;
+}
+
 bool replay_plan(const AttnArgs& a, int dtype, ReplayPlan& plan) {
   FusedPlan fp;
   if (!fast_plan(a, dtype, fp)) return false;
@@ -1433,6 +1456,7 @@ void append_fast_resources(std::string& out) {
     out += buf;
   };
   for (const auto& e : g_fast) plan_row(e);
+  for (const auto& e : g_fast_small) plan_row(e);
   for (const auto& e : g_rt2) plan_row(e);
 }
 

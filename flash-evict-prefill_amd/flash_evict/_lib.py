@@ -51,6 +51,7 @@ _SIGNATURES = {
     "fe_fused_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "fe_fused_timing_read": (ctypes.c_int, [_I64P, ctypes.POINTER(ctypes.c_double)]),
     "fe_kernel_resources": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t]),
+    "fe_last_plan": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t]),
     "fe_last_error": (ctypes.c_char_p, []),
     "fe_abi_version": (ctypes.c_int, []),
 }

@@ -215,6 +215,15 @@ int fe_fused_timing_read(int64_t* launches, double* total_ms);
 /* JSON description of the device kernels (registers, LDS, scratch), written to buf. */
 int fe_kernel_resources(char* buf, size_t cap);
 
+/*
+ * Names of the attention (+ replay) kernels the calling thread's last fe_prefill,
+ * fe_prefill_ws or fe_prefill_static launched, e.g. "attn_rt2<bf16,128> + replay_fast<bf16,128>"
+ * ("" before any such call), written to buf with its terminating zero. No counterpart in the
+ * reference (benchmark support: which kernels a timing covers). FE_ERR_INVALID when cap is
+ * too small.
+ */
+int fe_last_plan(char* buf, size_t cap);
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* fe_last_error(void);
 

@@ -120,3 +120,33 @@ def test_dynamic_and_static_schedules_agree(b, hq, hk, n, d, dtype, causal, weig
     o_st0, _ = _run(q, k, v, causal, weighted, decay, window, use_ws=True, ws_bytes=0, score=False)
     assert torch.equal(o_dyn0, o_st0)
     assert torch.equal(o_dyn0, o_dyn)
+
+
+def _last_plan():
+    import ctypes
+    buf = ctypes.create_string_buffer(256)
+    _lib.check(_lib.lib().fe_last_plan(buf, len(buf)), "fe_last_plan")
+    return buf.value.decode()
+
+
+@pytest.mark.parametrize("d", [64, 32])
+def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
+    """Tile dims 32 and 64 run the 4-wave small-grid attention kernel when the 8-wave kernel's
+    items would fill at most two rounds of its resident workgroups. Both compute every row tile
+    the same way (one row tile per wave, 64-key tiles), so batch 0 of a launch big enough for
+    the 8-wave kernel equals the small launch of the same data bitwise; the importance differs
+    only by FP32 atomic order. fe_last_plan names the kernels each launch ran."""
+    hq, hk, n = 4, 2, 2048
+    print(f"small-grid vs 8-wave attention kernel d={d} hq={hq} hk={hk} n={n}", flush=True)
+    q = seeded_randn((40, hq, n, d), torch.bfloat16, 17 + d)
+    k = seeded_randn((40, hk, n, d), torch.bfloat16, 18 + d)
+    v = seeded_randn((40, hk, n, d), torch.bfloat16, 19 + d)
+    o_small, i_small = _run(q[:1], k[:1], v[:1], True, True, 0.0, 0, use_ws=True)
+    small_plan = _last_plan()
+    o_big, i_big = _run(q, k, v, True, True, 0.0, 0, use_ws=True)
+    big_plan = _last_plan()
+    assert small_plan == "attn_fast4<bf16,%d> + replay_fast<bf16,%d>" % (d, d), small_plan
+    assert big_plan == "attn_fast<bf16,%d> + replay_fast<bf16,%d>" % (d, d), big_plan
+    assert torch.equal(o_small, o_big[:1])
+    scale = i_big[:1].abs().amax(dim=-1, keepdim=True)
+    assert ((i_small - i_big[:1]).abs() <= 2e-6 * i_big[:1].abs() + 1e-6 * scale).all()
