@@ -34,6 +34,8 @@ struct AttnArgs {
   int nitems;                       // dynamic schedule: work items of the launch
   int nstatic;                      // dynamic schedule: workgroups launched (each starts with item blockIdx.x)
   int tail;                         // dynamic schedule: first item of the queues' light parts (nitems: none)
+  int nattn;                        // attention items; items past them are replay items (attn_rt2_kernel)
+  unsigned* done;                   // replay items: one bit per attention item, set once its biases are out
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
 };
 
@@ -41,10 +43,14 @@ struct AttnArgs {
 // next 256-byte boundary after the replay biases): eight per kernel (one per XCD queue), each
 // on its own 128-byte line, the attention kernel's from word 0 and the replay kernel's from
 // word kQueueReplay; a queue's counters are the 64-bit words at ints 0 and 2 of its line (its
-// heavy and light parts, take_item in fe_attn_fast.hip). Zeroed before every launch.
+// heavy and light parts, take_item in fe_attn_fast.hip). Then, from word kQueueDone, one bit per
+// attention item for the replay items of attn_rt2_kernel (kMaxDoneItems bits). Zeroed before
+// every launch.
 constexpr int kQueueStride = 32;
 constexpr int kQueueReplay = 8 * kQueueStride;
-constexpr int kQueueWords = 2 * kQueueReplay;
+constexpr int kQueueDone = 2 * kQueueReplay;
+constexpr int kMaxDoneItems = 16384;
+constexpr int kQueueWords = kQueueDone + kMaxDoneItems / 32;
 constexpr size_t kQueueBytes = kQueueWords * sizeof(int);
 // s_getreg_b32 operand of hwreg(HW_REG_XCC_ID): register 20, bits 0-31 (the XCC index is bits 0-3)
 constexpr int kHwRegXccId = (31 << 11) | 20;

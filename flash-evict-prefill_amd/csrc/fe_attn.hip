@@ -689,6 +689,15 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #define FE_SMALL_GRID_ROUNDS 2
 #endif
 
+// Replay items in the two-row-tile attention launch (prefill_impl) for observation windows of at
+// most this share of the rows. Build options, for measurement.
+#ifndef FE_REPLAY_ITEMS
+#define FE_REPLAY_ITEMS 1
+#endif
+#ifndef FE_REPLAY_ITEMS_MAX
+#define FE_REPLAY_ITEMS_MAX 0.25
+#endif
+
 // Key tiles of the query rows of row tiles [.., t_end) of one (batch, KV head): causal rows see
 // keys up to their own position.
 int64_t item_key_tiles(int64_t t_end, int64_t G, int64_t N, bool causal) {
@@ -774,6 +783,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.nitems = 0;
   a.nstatic = 0;
   a.tail = 0;
+  a.nattn = 0x7fffffff;
+  a.done = nullptr;
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -882,6 +893,31 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     });
     grid = a.nstatic;
   }
+  // Short observation windows on the two-row-tile attention kernel: the replay runs as work
+  // items of the attention launch, numbered after its attention items (so in every XCD queue
+  // they follow them), each waiting for its rows' attention item to publish their biases (a bit
+  // per attention item after the counters). They fill the end of the attention launch, where
+  // the replay kernel would start only once the last attention item is done. Item = (batch and
+  // KV head, row group of 16 row tiles holding window rows, key range): key ranges chosen for
+  // about four items per resident workgroup, of at least eight key tiles where the keys allow
+  // (a window of 128 rows at N = 32K otherwise made items of two tiles, 0.4% slower overall).
+  bool replay_items = false;
+  if (FE_REPLAY_ITEMS && split && ctr && plan.rows == 16 && items <= kMaxDoneItems &&
+      (double)(N - a.win_lo) <= FE_REPLAY_ITEMS_MAX * (double)N) {
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / 16;
+    const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
+    const int64_t max_tiles = (N + 63) / 64;
+    const int64_t rs_max = (max_tiles + 7) / 8;
+    int64_t rs = (4 * (int64_t)a.nstatic + nwg - 1) / nwg;
+    rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
+    if (items + nwg * rs < (int64_t)0x7fffffff) {
+      replay_items = true;
+      a.nattn = (int)items;
+      a.nitems = (int)(items + nwg * rs);
+      a.rsplit = (int)rs;
+      a.done = (unsigned*)(ctr + kQueueDone);
+    }
+  }
   if (score || ctr) {
     err = launch_zero(score ? importance : nullptr, score ? B * Hkv * N : 0, ctr, ctr ? kQueueWords : 0, stream);
     if (err != hipSuccess) {
@@ -915,14 +951,15 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       return FE_ERR_HIP;
     }
   }
-  g_last_plan = split ? std::string(plan.name) + " + " + rplan.name : std::string(plan.name);
+  g_last_plan = replay_items ? std::string(plan.name) + " with replay items"
+                : (split ? std::string(plan.name) + " + " + rplan.name : std::string(plan.name));
   void* kargs[] = {&a};
   err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
   if (err != hipSuccess) {
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;
   }
-  if (split) {
+  if (split && !replay_items) {
     // Workgroups of rplan.rows row tiles; only those holding window rows are launched
     // (tiles before query block win_lo/32 have none), heaviest first.
     AttnArgs r = a;

@@ -16,7 +16,7 @@ namespace fe {
 namespace {
 
 // FE_STATIC_BIAS_ROWS floats of replay biases plus the dynamic schedule's item counters (16 MiB
-// + 2 KiB) on every GPU fe_prefill_static runs on, held until the process ends. Its contents
+// + 4 KiB) on every GPU fe_prefill_static runs on, held until the process ends. Its contents
 // persist between calls (the last call's biases and counters); the attention kernel writes every
 // bias the replay kernel reads, and each call zeroes the counters (with a fill kernel) before its
 // kernels run.

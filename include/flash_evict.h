@@ -83,7 +83,7 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
 /*
  * fe_prefill with a caller-provided workspace (same contract). fe_prefill_workspace_bytes()
  * is B*Hq*N floats of replay biases (score != 0; none otherwise), rounded up to 256 bytes,
- * plus 2 KiB of work-item counters. With the fast layouts (D a multiple of 8 up to 256,
+ * plus 4 KiB of work-item counters. With the fast layouts (D a multiple of 8 up to 256,
  * nonzero scale, unit-stride 16-byte aligned K/V rows; Q of any strides):
  *   * the replay runs as a second kernel at higher occupancy: the attention kernel leaves the
  *     per-row replay bias m_q + log2 l_q - decay*log2(e)*(q-N+1) in the workspace;
@@ -92,6 +92,11 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  *     up (the call zeroes them first), instead of one per workgroup index. Each item is
  *     computed the same way whichever workgroup takes it: the output is bitwise that of the
  *     static schedule, the importance equal up to FP32 atomic order;
+ *   * with the whole workspace and a short observation window (at most a quarter of the rows
+ *     replayed) at head dims 72..128, the replay runs as work items of the attention launch
+ *     instead of a second kernel (same arithmetic: output bitwise equal, importance equal up
+ *     to FP32 atomic order); they wait for their rows' attention items, so that launch needs
+ *     all its workgroups resident at once, as it has on a GPU no other kernel shares;
  *   * score == 0 uses the counters alone;
  *   * a zero scale runs on the fast kernels with Q zeroed at load (every logit exactly 0).
  * At head dims 72..128 (multiples of 8) the split schedule's attention kernel holds two row
@@ -129,7 +134,7 @@ int fe_prefill_ws(const void* q, const void* k, const void* v, void* out, float*
  * routine (and no timing events: fe_fused_timing_enable does not apply to it). No
  * counterpart in the reference; it is for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The buffer holds FE_STATIC_BIAS_ROWS floats and the work-item counters (16 MiB + 2 KiB) on
+ * The buffer holds FE_STATIC_BIAS_ROWS floats and the work-item counters (16 MiB + 4 KiB) on
  * every GPU this entry point has run on, from its first call there until the process ends
  * (processes that never call it do not hold the buffer). A scoring call needs
  * B*Hq*N <= FE_STATIC_BIAS_ROWS and otherwise fails with FE_ERR_WORKSPACE before launching

@@ -21,11 +21,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _ws_layout(b, h, n, score):
-    """fe_prefill_workspace_bytes: B*Hq*N floats of replay biases (scoring calls), then 2 KiB
+    """fe_prefill_workspace_bytes: B*Hq*N floats of replay biases (scoring calls), then 4 KiB
     of work-item counters for the dynamic schedule (eight queues per kernel, one counter per
     128-byte line) at the next 256-byte boundary."""
     bias = b * h * n * 4 if score else 0
-    return (bias + 255) // 256 * 256 + 2048
+    return (bias + 255) // 256 * 256 + 4096
 
 
 def _run(q, k, v, causal, weighted, decay, window, use_ws, ws_bytes=None, score=True):
@@ -150,3 +150,29 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     assert torch.equal(o_small, o_big[:1])
     scale = i_big[:1].abs().amax(dim=-1, keepdim=True)
     assert ((i_small - i_big[:1]).abs() <= 2e-6 * i_big[:1].abs() + 1e-6 * scale).all()
+
+
+@pytest.mark.parametrize("b,hq,hk,n,d,dtype,causal,decay,window", [
+    (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.1, 0),       # llama8k's schedule: 1050 rows replayed
+    (2, 8, 2, 3000, 120, torch.float16, True, 0.0, 200),      # partial tile dim, ragged N, fp16
+    (1, 16, 2, 2048, 96, torch.bfloat16, False, 0.0, 100),    # tile dim 96, non-causal
+])
+def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, decay, window):
+    """Short observation windows on the two-row-tile attention kernel run the replay as work
+    items of the attention launch (the whole workspace); a workspace of the replay biases alone
+    runs the separate replay kernel. Same attention items and the same replay arithmetic: the
+    output is bitwise equal and the importance equal up to FP32 atomic order. fe_last_plan names
+    the schedule each launch ran."""
+    print(f"replay items vs replay kernel b={b} hq={hq} hk={hk} n={n} d={d} {dtype} causal={causal} "
+          f"decay={decay} window={window}", flush=True)
+    q = seeded_randn((b, hq, n, d), dtype, 5 * n + d)
+    k = seeded_randn((b, hk, n, d), dtype, 5 * n + d + 1)
+    v = seeded_randn((b, hk, n, d), dtype, 5 * n + d + 2)
+    o_it, i_it = _run(q, k, v, causal, True, decay, window, use_ws=True)
+    plan_it = _last_plan()
+    o_rk, i_rk = _run(q, k, v, causal, True, decay, window, use_ws=True, ws_bytes=b * hq * n * 4)
+    plan_rk = _last_plan()
+    assert plan_it.endswith(" with replay items") and plan_it.startswith("attn_rt2<"), plan_it
+    assert " + replay_fast<" in plan_rk, plan_rk
+    assert torch.equal(o_it, o_rk)
+    assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())

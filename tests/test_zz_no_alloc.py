@@ -176,7 +176,7 @@ print("RESERVED_BY_STATIC", rc, free_after_ws - free_after_static)
 
 @pytest.mark.gpu
 def test_static_buffer_reserved_only_by_static_entry():
-    """The static workspace (16 MiB + 2 KiB per GPU) lives in a code object of its own: a process
+    """The static workspace (16 MiB + 4 KiB per GPU) lives in a code object of its own: a process
     holds it only once it calls fe_prefill_static, not from its first prefill() call. Checked in a
     fresh process (device free memory after prefill() calls, then after one static call)."""
     import os
