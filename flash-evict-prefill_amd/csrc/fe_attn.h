@@ -36,6 +36,7 @@ struct AttnArgs {
   int tail;                         // dynamic schedule: first item of the queues' light parts (nitems: none)
   int nattn;                        // attention items; items past them are replay items (attn_rt2_kernel)
   unsigned* done;                   // replay items: one bit per attention item, set once its biases are out
+  int wait_base, wait_per_tile;     // replay items: polls of a dependency's bit (plus per key tile) before running it
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed
 };
 

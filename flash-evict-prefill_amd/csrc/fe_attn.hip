@@ -33,6 +33,7 @@
 //     different KV heads (the hardware deals blocks round-robin over the 8 XCDs, so each
 //     XCD's L2 sees a small set of KV heads).
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #include <mutex>
 #include <string>
@@ -697,6 +698,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_REPLAY_ITEMS_MAX
 #define FE_REPLAY_ITEMS_MAX 0.25
 #endif
+#ifndef FE_COOP_LAUNCH
+#define FE_COOP_LAUNCH 0
+#endif
 
 // Key tiles of the query rows of row tiles [.., t_end) of one (batch, KV head): causal rows see
 // keys up to their own position.
@@ -785,6 +789,15 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.tail = 0;
   a.nattn = 0x7fffffff;
   a.done = nullptr;
+  // Polls of a replay item's dependency before it runs the attention item itself: 4096 plus 64
+  // per key tile (each poll sleeps about 0.27 us). FLASH_EVICT_REPLAY_WAIT=0 makes every replay
+  // item run its dependency at once (tests of that path).
+  {
+    const char* w = getenv("FLASH_EVICT_REPLAY_WAIT");
+    const bool none = w && w[0] == '0' && w[1] == 0;
+    a.wait_base = none ? 0 : 4096;
+    a.wait_per_tile = none ? 0 : 64;
+  }
   for (int i = 0; i < 4; ++i) {
     a.qs[i] = q_strides[i];
     a.ks[i] = k_strides[i];
@@ -954,7 +967,24 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   g_last_plan = replay_items ? std::string(plan.name) + " with replay items"
                 : (split ? std::string(plan.name) + " + " + rplan.name : std::string(plan.name));
   void* kargs[] = {&a};
-  err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
+  if (replay_items && FE_COOP_LAUNCH) {
+    // a cooperative launch fails rather than start with some workgroups not resident, which the
+    // replay items' waits need; on failure the call runs the replay kernel instead
+    err = hipLaunchCooperativeKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, (unsigned)plan.lds,
+                                     stream);
+    if (err != hipSuccess) {
+      (void)hipGetLastError();
+      replay_items = false;
+      a.nattn = 0x7fffffff;
+      a.nitems = (int)items;
+      a.rsplit = 1;
+      a.done = nullptr;
+      g_last_plan = std::string(plan.name) + " + " + rplan.name;
+      err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
+    }
+  } else {
+    err = hipLaunchKernel(plan.fn, dim3((unsigned)grid), dim3(64 * plan.waves), kargs, plan.lds, stream);
+  }
   if (err != hipSuccess) {
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;

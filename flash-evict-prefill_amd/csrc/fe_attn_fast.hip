@@ -758,23 +758,31 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
 
 
 // Replay items of attn_rt2_kernel (short observation windows): lane 0 of the calling wave waits
-// until attention item `dep` has published its rows' replay biases (its bit in a.done). The bias
-// words are written and read as agent-scope relaxed atomics (write-through stores and loads
-// that bypass a stale L2 line), the writer waits for its stores before its workgroup sets the
-// bit, and the waiting lane's load of the bit completes before the workgroup barrier that
-// precedes the bias loads, so a bias read after the bit is seen is the one written. The wait is
-// bounded (about a second at the sleep below); it ends at once in practice: attention items are
-// numbered before replay items in every queue, and the window rows a replay item needs are
-// the heaviest attention items, taken first.
-__device__ __forceinline__ void wait_item_done(const AttnArgs& a, int dep) {
+// until attention item `dep` has published its rows' replay biases (its bit in a.done) and
+// returns whether it has. The bias words are written and read as agent-scope relaxed atomics
+// (write-through stores and loads that bypass a stale L2 line), the writer waits for its stores
+// before its workgroup sets the bit, and the waiting lane's load of the bit completes before the
+// workgroup barrier that precedes the bias loads, so a bias read after the bit is seen is the
+// one written. Attention items are numbered before replay items in every queue and the window
+// rows a replay item needs are the heaviest attention items, taken first, so the wait is short;
+// it is bounded by about 17 us per key tile of the dependency (five times what a tile takes;
+// a.wait_base + a.wait_per_tile polls of about 0.27 us),
+// and when it runs out (the dependency's workgroup not resident, say, on a GPU another kernel
+// shares) the caller computes the dependency itself: an attention item writes the same output
+// and biases whoever runs it.
+__device__ __forceinline__ bool wait_item_done(const AttnArgs& a, int dep, int dep_tiles) {
+  bool ok = true;
   if (lane_now() == 0) {
     const unsigned bit = 1u << (dep & 31);
     unsigned* w = a.done + (dep >> 5);
-    for (int spin = 0; spin < (1 << 22); ++spin) {
-      if (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & bit) break;
-      __builtin_amdgcn_s_sleep(8);
+    const int polls = a.wait_base + a.wait_per_tile * dep_tiles;
+    ok = false;
+    for (int spin = 0; spin < polls && !ok; ++spin) {
+      ok = (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & bit) != 0;
+      if (!ok) __builtin_amdgcn_s_sleep(8);
     }
   }
+  return ok;
 }
 
 // Traversal 1 (reference flash_evict/prefill.py:37-60) with two row tiles per wave (attention
@@ -817,162 +825,11 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
-  __shared__ int s_item;
+  __shared__ int s_item, s_ready;
   int item = (int)blockIdx.x;
   const int item_end = a.queue ? a.nitems : item + 1;
-  for (; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end) {
-    if (item >= a.nattn) {
-      // ---------------- replay item (reference flash_evict/prefill.py:61-83), short observation
-      // windows: the window rows of one attention item's 16 row tiles against one key range.
-      // S = Q K^T with lanes holding keys, exp2(s * scale*log2e - b_q) summed over the rows of
-      // each key in-lane and over the waves in LDS, one FP32 atomic per key and tile: the
-      // arithmetic of replay_fast_kernel, here in the attention kernel's workgroups, so the
-      // replay fills the end of the attention launch instead of following it.
-      const int ritem = item - a.nattn;
-      const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
-      int BH = a.BH, G = a.G, Hkv = a.Hkv, rsplit = a.rsplit;
-      asm volatile("" : "+s"(BH), "+s"(G), "+s"(Hkv), "+s"(rsplit));
-      const int bh = (int)((unsigned)ritem % (unsigned)BH);
-      const int rest = (int)((unsigned)ritem / (unsigned)BH);
-      const int ks = rest % rsplit;
-      const int wg = a.wg_bh - 1 - rest / rsplit;
-      const int b = bh / Hkv, hkv = bh - b * Hkv;
-      const int t_begin = wg * (NW * RT);
-      const int t_end = min(a.tiles_bh, t_begin + NW * RT);
-      const int kv_end = a.causal ? min(N, ((t_end - 1) / G + 1) * 32) : N;
-      const int ntiles_all = (kv_end + BN - 1) / BN;
-      const int per = (ntiles_all + rsplit - 1) / rsplit;
-      const int it_lo = ks * per, it_hi = min(ntiles_all, it_lo + per);
-      // the attention item of these rows (same decode) publishes their biases
-      if (wv == 0) wait_item_done(a, (a.wg_bh - 1 - wg) * BH + bh);
-      __syncthreads();
-      if (it_lo >= it_hi) continue;
-
-      int q0[RT];
-      bool tv[RT];
-      u32x4 qf[RT][NDC];
-      float nb[RT][16];
-      int rwave_hi = -1;                       // last key this wave's window rows see
-      const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
-  #pragma unroll
-      for (int j = 0; j < RT; ++j) {
-        const int t = t_begin + RT * wv + j;
-        tv[j] = t < t_end;
-        const int tt = tv[j] ? t : t_begin;
-        q0[j] = (tt / G) * 32;
-        const int head = hkv * G + (tt - (tt / G) * G);
-        const bool rin = tv[j] && q0[j] + 31 >= a.win_lo;
-        if (rin) rwave_hi = max(rwave_hi, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
-        const int qr = q0[j] + l32;
-        const bool ok = rin && qr < N;
-        const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
-  #pragma unroll
-        for (int c = 0; c < NDC; ++c)
-          qf[j][c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg)
-                        : (u32x4){0u, 0u, 0u, 0u};
-        const float br = ok ? __hip_atomic_load(a.bias + (long long)(b * a.Hq + head) * N + qr, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT)
-                            : POS_INF;
-        // minus the biases of the 16 rows a lane holds (register i: row 8(i/4) + 4h + i%4)
-  #pragma unroll
-        for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
-      }
-      const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
-      const u32 krow = (u32)(a.ks[2] * 2);
-      const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
-      float* imp_row = a.imp + (long long)bh * N;
-      auto r_dma = [&](int kb, unsigned char* ldst) {
-        const int ln = lane_now();
-        const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
-        dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
-      };
-      // wave SLOT adds up slot SLOT of the pair from it0 in buffer BUF over the waves
-      auto r_flush = [&](int it0, int BUF) __attribute__((always_inline)) {
-        if (wv < SLOTS && it0 + wv < it_hi) {
-          const int ln = lane_now();
-          const float* rr = red + ((BUF * SLOTS + wv) * NW) * BN + ln;
-          float sum = 0.f;
-  #pragma unroll
-          for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
-          const int key = (it0 + wv) * BN + ln;
-          if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
-        }
-      };
-      auto r_sync = [&](int it, int BUF) __attribute__((always_inline)) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (it > it_lo) r_flush(it - SLOTS, BUF ^ 1);
-        if (dmaw) {
-  #pragma unroll
-          for (int sl = 0; sl < SLOTS; ++sl)
-            if (it + SLOTS + sl < it_hi) r_dma((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
-        }
-      };
-      auto r_tile = [&](int it, int BUF, int SLOT) __attribute__((always_inline)) {
-        const int kb = it * BN;
-        float cs[2] = {0.f, 0.f};
-        const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
-  #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          if (kb + 32 * s > rwave_hi) continue;
-          f32x16 sacc[RT];
-  #pragma unroll
-          for (int j = 0; j < RT; ++j) sacc[j] = (f32x16){};
-  #pragma unroll
-          for (int c = 0; c < NDC; ++c) {
-            const u32x4 kf = *(const u32x4*)(kt + c * 2048 + s * 1024 + koff);
-  #pragma unroll
-            for (int j = 0; j < RT; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
-          }
-          float c4[4];
-  #pragma unroll
-          for (int j = 0; j < RT; ++j) {
-            // lanes hold key kb + 32s + l32; causal mask on diagonal halves
-            if (a.causal && kb + 32 * s + 31 > q0[j]) {
-              const int ln = lane_now();
-              const int rel = (ln & 31) - 4 * (ln >> 5) + (kb + 32 * s - q0[j]);
-  #pragma unroll
-              for (int i = 0; i < 16; ++i) sacc[j][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[j][i];
-            }
-  #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const float e = fast_exp2(fmaf(sacc[j][i], a.abs_scale_log2, nb[j][i]));
-              if (j == 0 && i < 4)
-                c4[i] = e;
-              else
-                c4[i & 3] += e;
-            }
-          }
-          cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
-        }
-        cs[0] = half_swap_sum(cs[0]);
-        cs[1] = half_swap_sum(cs[1]);
-        if (hh == 0) {
-          float* rb = red + ((BUF * SLOTS + SLOT) * NW + wv) * BN;
-          rb[l32] = cs[0];
-          rb[32 + l32] = cs[1];
-        }
-      };
-      if (dmaw) {
-  #pragma unroll
-        for (int sl = 0; sl < SLOTS; ++sl)
-          if (it_lo + sl < it_hi) r_dma((it_lo + sl) * BN, lds_k0 + sl * TILE);
-      }
-      for (int it = it_lo; it < it_hi; it += 2 * SLOTS) {
-        r_sync(it, 0);
-        r_tile(it, 0, 0);
-        if (it + 1 < it_hi) r_tile(it + 1, 0, 1);
-        if (it + SLOTS < it_hi) {
-          r_sync(it + SLOTS, 1);
-          r_tile(it + SLOTS, 1, 0);
-          if (it + SLOTS + 1 < it_hi) r_tile(it + SLOTS + 1, 1, 1);
-        }
-      }
-      __syncthreads();
-      const int last = it_lo + ((it_hi - 1 - it_lo) / SLOTS) * SLOTS;
-      r_flush(last, ((last - it_lo) / SLOTS) & 1);
-      continue;
-    }
+  // One attention item (traversal 1 of its 16 row tiles, the output, the replay biases).
+  auto run_attention = [&](const int item) __attribute__((always_inline)) {
     const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
     // The divisors of the item decode, taken opaquely: otherwise the compiler keeps their
     // reciprocals, computed once before the item loop, in registers across it.
@@ -1297,6 +1154,172 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       if (wv == 0 && lane_now() == 0)
         __hip_atomic_fetch_or(a.done + (item >> 5), 1u << (item & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  };
+
+  for (; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end) {
+    if (item < a.nattn) {
+      run_attention(item);
+      continue;
+    }
+      // ---------------- replay item (reference flash_evict/prefill.py:61-83), short observation
+      // windows: the window rows of one attention item's 16 row tiles against one key range.
+      // S = Q K^T with lanes holding keys, exp2(s * scale*log2e - b_q) summed over the rows of
+      // each key in-lane and over the waves in LDS, one FP32 atomic per key and tile: the
+      // arithmetic of replay_fast_kernel, here in the attention kernel's workgroups, so the
+      // replay fills the end of the attention launch instead of following it.
+      const int ritem = item - a.nattn;
+      const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
+      int BH = a.BH, G = a.G, Hkv = a.Hkv, rsplit = a.rsplit;
+      asm volatile("" : "+s"(BH), "+s"(G), "+s"(Hkv), "+s"(rsplit));
+      const int bh = (int)((unsigned)ritem % (unsigned)BH);
+      const int rest = (int)((unsigned)ritem / (unsigned)BH);
+      const int ks = rest % rsplit;
+      const int wg = a.wg_bh - 1 - rest / rsplit;
+      const int b = bh / Hkv, hkv = bh - b * Hkv;
+      const int t_begin = wg * (NW * RT);
+      const int t_end = min(a.tiles_bh, t_begin + NW * RT);
+      const int kv_end = a.causal ? min(N, ((t_end - 1) / G + 1) * 32) : N;
+      const int ntiles_all = (kv_end + BN - 1) / BN;
+      const int per = (ntiles_all + rsplit - 1) / rsplit;
+      const int it_lo = ks * per, it_hi = min(ntiles_all, it_lo + per);
+      // the attention item of these rows (same decode) publishes their biases; if it has not
+      // within the bound, this workgroup runs it
+      const int dep = (a.wg_bh - 1 - wg) * BH + bh;
+      if (wv == 0) {
+        const bool ok = wait_item_done(a, dep, ntiles_all);
+        if (lane_now() == 0) s_ready = ok ? 1 : 0;
+      }
+      __syncthreads();
+      if (!__builtin_amdgcn_readfirstlane(s_ready)) {
+        run_attention(dep);
+        __syncthreads();
+      }
+      if (it_lo >= it_hi) continue;
+
+      int q0[RT];
+      bool tv[RT];
+      u32x4 qf[RT][NDC];
+      float nb[RT][16];
+      int rwave_hi = -1;                       // last key this wave's window rows see
+      const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
+  #pragma unroll
+      for (int j = 0; j < RT; ++j) {
+        const int t = t_begin + RT * wv + j;
+        tv[j] = t < t_end;
+        const int tt = tv[j] ? t : t_begin;
+        q0[j] = (tt / G) * 32;
+        const int head = hkv * G + (tt - (tt / G) * G);
+        const bool rin = tv[j] && q0[j] + 31 >= a.win_lo;
+        if (rin) rwave_hi = max(rwave_hi, a.causal ? min(q0[j] + 31, N - 1) : N - 1);
+        const int qr = q0[j] + l32;
+        const bool ok = rin && qr < N;
+        const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+  #pragma unroll
+        for (int c = 0; c < NDC; ++c)
+          qf[j][c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg)
+                        : (u32x4){0u, 0u, 0u, 0u};
+        const float br = ok ? __hip_atomic_load(a.bias + (long long)(b * a.Hq + head) * N + qr, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : POS_INF;
+        // minus the biases of the 16 rows a lane holds (register i: row 8(i/4) + 4h + i%4)
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) nb[j][i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+      }
+      const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+      const u32 krow = (u32)(a.ks[2] * 2);
+      const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+      float* imp_row = a.imp + (long long)bh * N;
+      auto r_dma = [&](int kb, unsigned char* ldst) {
+        const int ln = lane_now();
+        const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
+        dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
+      };
+      // wave SLOT adds up slot SLOT of the pair from it0 in buffer BUF over the waves
+      auto r_flush = [&](int it0, int BUF) __attribute__((always_inline)) {
+        if (wv < SLOTS && it0 + wv < it_hi) {
+          const int ln = lane_now();
+          const float* rr = red + ((BUF * SLOTS + wv) * NW) * BN + ln;
+          float sum = 0.f;
+  #pragma unroll
+          for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
+          const int key = (it0 + wv) * BN + ln;
+          if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+        }
+      };
+      auto r_sync = [&](int it, int BUF) __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (it > it_lo) r_flush(it - SLOTS, BUF ^ 1);
+        if (dmaw) {
+  #pragma unroll
+          for (int sl = 0; sl < SLOTS; ++sl)
+            if (it + SLOTS + sl < it_hi) r_dma((it + SLOTS + sl) * BN, (BUF == 0 ? lds_k1 : lds_k0) + sl * TILE);
+        }
+      };
+      auto r_tile = [&](int it, int BUF, int SLOT) __attribute__((always_inline)) {
+        const int kb = it * BN;
+        float cs[2] = {0.f, 0.f};
+        const unsigned char* kt = (BUF == 0 ? lds_k0 : lds_k1) + SLOT * TILE;
+  #pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (kb + 32 * s > rwave_hi) continue;
+          f32x16 sacc[RT];
+  #pragma unroll
+          for (int j = 0; j < RT; ++j) sacc[j] = (f32x16){};
+  #pragma unroll
+          for (int c = 0; c < NDC; ++c) {
+            const u32x4 kf = *(const u32x4*)(kt + c * 2048 + s * 1024 + koff);
+  #pragma unroll
+            for (int j = 0; j < RT; ++j) sacc[j] = E::mfma(qf[j][c], kf, sacc[j]);
+          }
+          float c4[4];
+  #pragma unroll
+          for (int j = 0; j < RT; ++j) {
+            // lanes hold key kb + 32s + l32; causal mask on diagonal halves
+            if (a.causal && kb + 32 * s + 31 > q0[j]) {
+              const int ln = lane_now();
+              const int rel = (ln & 31) - 4 * (ln >> 5) + (kb + 32 * s - q0[j]);
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) sacc[j][i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[j][i];
+            }
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const float e = fast_exp2(fmaf(sacc[j][i], a.abs_scale_log2, nb[j][i]));
+              if (j == 0 && i < 4)
+                c4[i] = e;
+              else
+                c4[i & 3] += e;
+            }
+          }
+          cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+        }
+        cs[0] = half_swap_sum(cs[0]);
+        cs[1] = half_swap_sum(cs[1]);
+        if (hh == 0) {
+          float* rb = red + ((BUF * SLOTS + SLOT) * NW + wv) * BN;
+          rb[l32] = cs[0];
+          rb[32 + l32] = cs[1];
+        }
+      };
+      if (dmaw) {
+  #pragma unroll
+        for (int sl = 0; sl < SLOTS; ++sl)
+          if (it_lo + sl < it_hi) r_dma((it_lo + sl) * BN, lds_k0 + sl * TILE);
+      }
+      for (int it = it_lo; it < it_hi; it += 2 * SLOTS) {
+        r_sync(it, 0);
+        r_tile(it, 0, 0);
+        if (it + 1 < it_hi) r_tile(it + 1, 0, 1);
+        if (it + SLOTS < it_hi) {
+          r_sync(it + SLOTS, 1);
+          r_tile(it + SLOTS, 1, 0);
+          if (it + SLOTS + 1 < it_hi) r_tile(it + SLOTS + 1, 1, 1);
+        }
+      }
+      __syncthreads();
+      const int last = it_lo + ((it_hi - 1 - it_lo) / SLOTS) * SLOTS;
+      r_flush(last, ((last - it_lo) / SLOTS) & 1);
+      continue;
   }
 }
 

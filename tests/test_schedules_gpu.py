@@ -176,3 +176,22 @@ def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, de
     assert " + replay_fast<" in plan_rk, plan_rk
     assert torch.equal(o_it, o_rk)
     assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())
+
+
+def test_replay_item_runs_its_dependency_when_the_wait_runs_out(monkeypatch):
+    """A replay item whose attention item has not published its biases within the wait's bound
+    runs that attention item itself (attention items are idempotent: whoever runs one writes the
+    same output and biases). FLASH_EVICT_REPLAY_WAIT=0 makes every replay item take that path at
+    once; the results equal the replay kernel's (bitwise output, importance up to FP32 atomic
+    order)."""
+    b, hq, hk, n, d = 1, 32, 8, 8192, 128
+    print(f"replay items running their dependencies b={b} hq={hq} hk={hk} n={n} d={d}", flush=True)
+    q = seeded_randn((b, hq, n, d), torch.bfloat16, 71)
+    k = seeded_randn((b, hk, n, d), torch.bfloat16, 72)
+    v = seeded_randn((b, hk, n, d), torch.bfloat16, 73)
+    o_rk, i_rk = _run(q, k, v, True, True, 0.1, 0, use_ws=True, ws_bytes=b * hq * n * 4)
+    monkeypatch.setenv("FLASH_EVICT_REPLAY_WAIT", "0")
+    o_it, i_it = _run(q, k, v, True, True, 0.1, 0, use_ws=True)
+    assert _last_plan().endswith(" with replay items")
+    assert torch.equal(o_it, o_rk)
+    assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())
