@@ -698,6 +698,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_REPLAY_ITEMS_MAX
 #define FE_REPLAY_ITEMS_MAX 0.25
 #endif
+#ifndef FE_REPLAY_ITEMS_PER_WG
+#define FE_REPLAY_ITEMS_PER_WG 2
+#endif
 #ifndef FE_COOP_LAUNCH
 #define FE_COOP_LAUNCH 0
 #endif
@@ -912,8 +915,9 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // per attention item after the counters). They fill the end of the attention launch, where
   // the replay kernel would start only once the last attention item is done. Item = (batch and
   // KV head, row group of 16 row tiles holding window rows, key range): key ranges chosen for
-  // about four items per resident workgroup, of at least eight key tiles where the keys allow
-  // (a window of 128 rows at N = 32K otherwise made items of two tiles, 0.4% slower overall).
+  // about two items per resident workgroup (four measured 1.3% slower at llama8k), of at least
+  // eight key tiles where the keys allow (a window of 128 rows at N = 32K otherwise made items of
+  // two tiles, 0.4% slower overall).
   bool replay_items = false;
   if (FE_REPLAY_ITEMS && split && ctr && plan.rows == 16 && items <= kMaxDoneItems &&
       (double)(N - a.win_lo) <= FE_REPLAY_ITEMS_MAX * (double)N) {
@@ -921,7 +925,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
     const int64_t max_tiles = (N + 63) / 64;
     const int64_t rs_max = (max_tiles + 7) / 8;
-    int64_t rs = (4 * (int64_t)a.nstatic + nwg - 1) / nwg;
+    int64_t rs = (FE_REPLAY_ITEMS_PER_WG * (int64_t)a.nstatic + nwg - 1) / nwg;
     rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
     if (items + nwg * rs < (int64_t)0x7fffffff) {
       replay_items = true;
