@@ -15,7 +15,7 @@ from flash_evict import prefill
 from oracle.attention import chunked
 from _helpers import (assert_importance_close, assert_schedules_agree, seeded_randn, split_runs_two_row_tiles,
                       transposed_qkv)
-from test_schedules_gpu import _run
+from test_schedules_gpu import _last_plan, _run
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +68,34 @@ def test_partial_head_dim_reads_stop_at_d(d):
         ref_out, ref_imp = chunked(q, k.contiguous(), v.contiguous(), block=512, dtype=torch.float64)
         assert (out.double() - ref_out.to(out.device)).abs().max().item() <= 2e-2
         assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+
+
+@pytest.mark.parametrize("d,scale,decay", [
+    (64, 0.69, 0.0),       # |scale| * log2 e just below 1
+    (64, 0.7, 0.02),       # just above 1
+    (48, None, 0.0),
+    (32, -0.3, 0.05),
+    (40, -1.0, 0.02),
+])
+def test_replay_scales_bf16(d, scale, decay):
+    """bf16 replay at tile dims 32 and 64 under the split schedule for scales around and above
+    1/log2(e) and negative ones, with and without a recency decay: against the float64 oracle
+    and against the fused single kernel (same attention kernel: bitwise-equal outputs)."""
+    n, hq, hk = 1500, 8, 2
+    print(f"bf16 replay d={d} scale={scale} decay={decay}", flush=True)
+    q = seeded_randn((1, hq, n, d), torch.bfloat16, 90 + d)
+    k = seeded_randn((1, hk, n, d), torch.bfloat16, 91 + d)
+    v = seeded_randn((1, hk, n, d), torch.bfloat16, 92 + d)
+    out, imp = prefill(q, k, v, scale=scale, recency_decay=decay)
+    tile = (d + 31) // 32 * 32
+    plan = _last_plan()
+    assert plan.endswith(" + replay_fast<bf16,%d%s>" % (tile, "" if d == tile else ",partial")), plan
+    ref_out, ref_imp = chunked(q, k, v, scale=scale, recency_decay=decay, block=512, dtype=torch.float64)
+    assert (out.double() - ref_out.to(out.device)).abs().max().item() <= 2e-2
+    assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)
+    o2, i2 = _run(q, k, v, True, True, decay, 0, use_ws=False, scale=(d ** -0.5 if scale is None else scale))
+    assert torch.equal(out, o2)
+    assert_schedules_agree(out, o2, imp, i2, v, hq, hk)
 
 
 def test_fast_head_dim_kernels_listed():

@@ -28,7 +28,7 @@ def _ws_layout(b, h, n, score):
     return (bias + 255) // 256 * 256 + 4096
 
 
-def _run(q, k, v, causal, weighted, decay, window, use_ws, ws_bytes=None, score=True):
+def _run(q, k, v, causal, weighted, decay, window, use_ws, ws_bytes=None, score=True, scale=None):
     b, h, n, d = q.shape
     hk = k.shape[1]
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -37,7 +37,8 @@ def _run(q, k, v, causal, weighted, decay, window, use_ws, ws_bytes=None, score=
     w = min(n, window or n)
     stream = torch.cuda.current_stream().cuda_stream
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), imp.data_ptr() if score else None, b, h, hk,
-            n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype], d ** -0.5, int(causal),
+            n, d, _lib.strides(q), _lib.strides(k), _lib.strides(v), _DTYPES[q.dtype],
+            d ** -0.5 if scale is None else scale, int(causal),
             int(weighted), int(score), decay, w)
     if use_ws:
         nbytes = L.fe_prefill_workspace_bytes(b, h, n, int(score))
@@ -63,6 +64,9 @@ CASES = [
     # more work items than resident workgroups: the queues' heavy and light parts and stealing
     # (attention 1024 items, replay 2048 with every row replayed)
     (1, 32, 8, 16384, 128, torch.bfloat16, True, True, 0.0, 0, "contiguous"),
+    # bf16 at tile dim 64 (D = 48: partial)
+    (1, 8, 2, 1000, 64, torch.bfloat16, True, True, 0.1, 0, "transposed"),
+    (2, 4, 2, 777, 48, torch.bfloat16, True, False, 0.0, 0, "contiguous"),
 ]
 
 
