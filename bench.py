@@ -18,10 +18,11 @@ nothing to the importance: 9.07 TFLOP executed at the headline (R = 1050).
 Prints one JSON line on stdout:
   value              = TFLOP the kernels execute per layer / measured layer time
   value_defined_work = the metric's defined TFLOP per layer / measured layer time
-  ms_per_step        = ms per layer (the metric's first half)
+  ms_per_step        = ms per layer (the metric's first half), timed without instrumentation
   roofline           = the attention + replay kernels alone: executed TFLOP / their mean
                        duration, timed with HIP events the library records on the kernels'
-                       own stream; frac = fraction of dense bf16 MFMA peak
+                       own stream over as many further layers; frac = fraction of dense bf16
+                       MFMA peak
   full_replay        = the same inputs with recency_decay 0 (every one of the 32768 rows
                        replayed, so executed = defined work): layer ms and the attention +
                        replay kernels' ms, TFLOP/s and fraction of peak, from the same run
@@ -215,9 +216,9 @@ def cpu_baseline(q, k, v, kw, executed_flop, sample_heads=8):
 
 def _timed_layers(step, steps, warmup, tag, warmup_ms=0.0):
     """Run at least `warmup` untimed layers, continuing back to back until `warmup_ms` of
-    warm-up have passed, then `steps` timed layers; return (ms per layer, fused-kernel ms per
-    launch, launches, warm-up layers run) with the fused kernels timed by the library's HIP
-    events.
+    warm-up have passed, then `steps` timed layers, then `steps` more with the library's HIP
+    events around the attention + replay kernels; return (ms per layer, those kernels' ms per
+    launch, launches, warm-up layers run).
 
     The minimum warm-up time is there for the GPU's power management: after a change of load
     the part first runs these kernels at a clock well below the one it then holds (measured on
@@ -242,14 +243,20 @@ def _timed_layers(step, steps, warmup, tag, warmup_ms=0.0):
         if time.perf_counter() - t_log > 0.5:
             t_log = time.perf_counter()
             log("%s warmup: %d layers, %.2f s" % (tag, done, t_log - t_start))
-    _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
-    _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
+    # the timed layers run without the library's timing events (each event record costs the
+    # stream about 6 us, 1.7% of a llama8k layer); the same number of layers follows with the
+    # events on, for the attention + replay kernels' own duration (roofline)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    _lib.check(L.fe_fused_timing_read(None, None), "fe_fused_timing_read")
+    _lib.check(L.fe_fused_timing_enable(1), "fe_fused_timing_enable")
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
     _lib.check(L.fe_fused_timing_enable(0), "fe_fused_timing_enable")
     launches = ctypes.c_int64(0)
     fused_ms = ctypes.c_double(0.0)
