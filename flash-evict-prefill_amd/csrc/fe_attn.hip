@@ -701,6 +701,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_REPLAY_ITEMS_PER_WG
 #define FE_REPLAY_ITEMS_PER_WG 2
 #endif
+#ifndef FE_TAIL_REPLAY_FRAC
+#define FE_TAIL_REPLAY_FRAC 0.03
+#endif
 #ifndef FE_COOP_LAUNCH
 #define FE_COOP_LAUNCH 0
 #endif
@@ -935,6 +938,32 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       a.done = (unsigned*)(ctr + kQueueDone);
     }
   }
+  // Longer windows: the heaviest FE_TAIL_REPLAY_FRAC (3%) of the row groups of each (batch, KV
+  // head) replay as items of the attention launch, where they fill its tail (their attention
+  // items are the first taken, so the biases are ready when they start); the replay kernel
+  // replays the rows below them (every row replayed: 0.2-1.4% faster pairs; 6% was slower).
+  int64_t tail_groups = 0;
+  if (FE_TAIL_REPLAY_FRAC > 0.0 && !replay_items && FE_REPLAY_ITEMS && split && ctr && plan.rows == 16 &&
+      items <= kMaxDoneItems && 16 % rplan.rows == 0) {
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / 16;
+    int64_t ng = (int64_t)ceil(FE_TAIL_REPLAY_FRAC * (double)((int64_t)a.wg_bh - wg_lo));
+    if (ng > (int64_t)a.wg_bh - wg_lo - 1) ng = (int64_t)a.wg_bh - wg_lo - 1;
+    if (ng > 0) {
+      const int64_t nwg = B * Hkv * ng;
+      const int64_t max_tiles = (N + 63) / 64;
+      const int64_t rs_max = (max_tiles + 7) / 8;
+      int64_t rs = (FE_REPLAY_ITEMS_PER_WG * (int64_t)a.nstatic + nwg - 1) / nwg;
+      rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
+      if (items + nwg * rs < (int64_t)0x7fffffff) {
+        replay_items = true;
+        tail_groups = ng;
+        a.nattn = (int)items;
+        a.nitems = (int)(items + nwg * rs);
+        a.rsplit = (int)rs;
+        a.done = (unsigned*)(ctr + kQueueDone);
+      }
+    }
+  }
   if (score || ctr) {
     err = launch_zero(score ? importance : nullptr, score ? B * Hkv * N : 0, ctr, ctr ? kQueueWords : 0, stream);
     if (err != hipSuccess) {
@@ -968,7 +997,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       return FE_ERR_HIP;
     }
   }
-  g_last_plan = replay_items ? std::string(plan.name) + " with replay items"
+  g_last_plan = replay_items ? std::string(plan.name) + " with replay items" + (tail_groups ? std::string(" + ") + rplan.name : std::string())
                 : (split ? std::string(plan.name) + " + " + rplan.name : std::string(plan.name));
   void* kargs[] = {&a};
   if (replay_items && FE_COOP_LAUNCH) {
@@ -979,6 +1008,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     if (err != hipSuccess) {
       (void)hipGetLastError();
       replay_items = false;
+      tail_groups = 0;
       a.nattn = 0x7fffffff;
       a.nitems = (int)items;
       a.rsplit = 1;
@@ -993,11 +1023,13 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     set_error(std::string("fe_prefill: fused kernel launch: ") + hipGetErrorString(err));
     return FE_ERR_HIP;
   }
-  if (split && !replay_items) {
+  if (split && (!replay_items || tail_groups)) {
     // Workgroups of rplan.rows row tiles; only those holding window rows are launched
-    // (tiles before query block win_lo/32 have none), heaviest first.
+    // (tiles before query block win_lo/32 have none), heaviest first; with tail groups, only
+    // the row tiles below them.
     AttnArgs r = a;
-    r.wg_bh = (int)((tiles_bh + rplan.rows - 1) / rplan.rows);
+    r.wg_bh = tail_groups ? (int)((((int64_t)a.wg_bh - tail_groups) * 16) / rplan.rows)
+                          : (int)((tiles_bh + rplan.rows - 1) / rplan.rows);
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / rplan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)r.wg_bh - wg_lo);
     // Split the keys of each workgroup when there are too few workgroups to fill the chip

@@ -160,13 +160,17 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.1, 0),       # llama8k's schedule: 1050 rows replayed
     (2, 8, 2, 3000, 120, torch.float16, True, 0.0, 200),      # partial tile dim, ragged N, fp16
     (1, 16, 2, 2048, 96, torch.bfloat16, False, 0.0, 100),    # tile dim 96, non-causal
+    # every row replayed: the heaviest row groups as items, the replay kernel for the others
+    (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.0, 0),
+    (2, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
 ])
 def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, decay, window):
     """Short observation windows on the two-row-tile attention kernel run the replay as work
-    items of the attention launch (the whole workspace); a workspace of the replay biases alone
-    runs the separate replay kernel. Same attention items and the same replay arithmetic: the
-    output is bitwise equal and the importance equal up to FP32 atomic order. fe_last_plan names
-    the schedule each launch ran."""
+    items of the attention launch (the whole workspace); longer ones run the heaviest row groups'
+    replay as items and the others on the replay kernel; a workspace of the replay biases alone
+    runs the separate replay kernel for every row. Same attention items and the same replay
+    arithmetic: the output is bitwise equal and the importance equal up to FP32 atomic order.
+    fe_last_plan names the schedule each launch ran."""
     print(f"replay items vs replay kernel b={b} hq={hq} hk={hk} n={n} d={d} {dtype} causal={causal} "
           f"decay={decay} window={window}", flush=True)
     q = seeded_randn((b, hq, n, d), dtype, 5 * n + d)
@@ -176,26 +180,31 @@ def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, de
     plan_it = _last_plan()
     o_rk, i_rk = _run(q, k, v, causal, True, decay, window, use_ws=True, ws_bytes=b * hq * n * 4)
     plan_rk = _last_plan()
-    assert plan_it.endswith(" with replay items") and plan_it.startswith("attn_rt2<"), plan_it
-    assert " + replay_fast<" in plan_rk, plan_rk
+    # at most a quarter of the rows replayed (fe_replay_rows): all of them as items
+    short = 4 * _lib.lib().fe_replay_rows(n, min(n, window or n), decay) <= n
+    assert plan_it.startswith("attn_rt2<") and " with replay items" in plan_it, plan_it
+    assert plan_it.endswith(" with replay items") == short, plan_it
+    assert " + replay_fast<" in plan_rk and " with replay items" not in plan_rk, plan_rk
     assert torch.equal(o_it, o_rk)
     assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())
 
 
-def test_replay_item_runs_its_dependency_when_the_wait_runs_out(monkeypatch):
+@pytest.mark.parametrize("decay", [0.1, 0.0])
+def test_replay_item_runs_its_dependency_when_the_wait_runs_out(monkeypatch, decay):
     """A replay item whose attention item has not published its biases within the wait's bound
     runs that attention item itself (attention items are idempotent: whoever runs one writes the
     same output and biases). FLASH_EVICT_REPLAY_WAIT=0 makes every replay item take that path at
     once; the results equal the replay kernel's (bitwise output, importance up to FP32 atomic
-    order)."""
+    order). Decay 0.1: every replayed row as items; decay 0: the heaviest row groups as items,
+    the others on the replay kernel."""
     b, hq, hk, n, d = 1, 32, 8, 8192, 128
-    print(f"replay items running their dependencies b={b} hq={hq} hk={hk} n={n} d={d}", flush=True)
+    print(f"replay items running their dependencies b={b} hq={hq} hk={hk} n={n} d={d} decay={decay}", flush=True)
     q = seeded_randn((b, hq, n, d), torch.bfloat16, 71)
     k = seeded_randn((b, hk, n, d), torch.bfloat16, 72)
     v = seeded_randn((b, hk, n, d), torch.bfloat16, 73)
-    o_rk, i_rk = _run(q, k, v, True, True, 0.1, 0, use_ws=True, ws_bytes=b * hq * n * 4)
+    o_rk, i_rk = _run(q, k, v, True, True, decay, 0, use_ws=True, ws_bytes=b * hq * n * 4)
     monkeypatch.setenv("FLASH_EVICT_REPLAY_WAIT", "0")
-    o_it, i_it = _run(q, k, v, True, True, 0.1, 0, use_ws=True)
-    assert _last_plan().endswith(" with replay items")
+    o_it, i_it = _run(q, k, v, True, True, decay, 0, use_ws=True)
+    assert " with replay items" in _last_plan()
     assert torch.equal(o_it, o_rk)
     assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())
