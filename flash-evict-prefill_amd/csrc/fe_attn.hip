@@ -684,10 +684,14 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #define FE_TAIL_REPLAY 0.0
 #endif
 
-// Rounds of resident workgroups up to which tile dims 32 and 64 run the small-grid attention
-// kernel (fast_plan_small). Build option, for measurement.
+// Rounds of resident workgroups up to which the small-grid attention kernel (fast_plan_small)
+// stands in: for the 8-wave kernel at tile dims 32 and 64, and for the two-row-tile kernel at 96
+// and 128. Build options, for measurement.
 #ifndef FE_SMALL_GRID_ROUNDS
 #define FE_SMALL_GRID_ROUNDS 2
+#endif
+#ifndef FE_SMALL_GRID_ROUNDS_RT2
+#define FE_SMALL_GRID_ROUNDS_RT2 1.0
 #endif
 
 // Replay items in the two-row-tile attention launch (prefill_impl) for observation windows of at
@@ -873,11 +877,15 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // Small grids at tile dims 32 and 64: where the 8-wave attention kernel's work items would
   // fill at most FE_SMALL_GRID_ROUNDS rounds of its resident workgroups, the 4-wave kernel
   // (twice the items, four workgroups per CU) fills the chip better.
+  // At tile dims 96 and 128, where the two-row-tile kernel's 16-row-tile items would not fill
+  // FE_SMALL_GRID_ROUNDS_RT2 rounds of its workgroups (one per CU), the 4-wave kernel (four row
+  // tiles per item, two workgroups per CU) does.
   FusedPlan small;
-  if (fast && plan.rows == 8 && fast_plan_small(a, dtype, small)) {
-    int64_t res8 = 0;
-    if (resident_blocks(plan.fn, 64 * plan.waves, plan.lds, stream, &res8) == hipSuccess &&
-        B * Hkv * ((tiles_bh + 7) / 8) <= (int64_t)FE_SMALL_GRID_ROUNDS * res8)
+  if (fast && (plan.rows == 8 || plan.rows == 16) && fast_plan_small(a, dtype, small)) {
+    int64_t res = 0;
+    const double rounds = plan.rows == 8 ? FE_SMALL_GRID_ROUNDS : FE_SMALL_GRID_ROUNDS_RT2;
+    if (resident_blocks(plan.fn, 64 * plan.waves, plan.lds, stream, &res) == hipSuccess &&
+        (double)(B * Hkv * ((tiles_bh + plan.rows - 1) / plan.rows)) <= rounds * (double)res)
       plan = small;
   }
   // Dynamic schedule (fast attention-only kernels, and the replay kernel): needs the

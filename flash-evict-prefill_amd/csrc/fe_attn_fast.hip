@@ -274,8 +274,8 @@ __device__ __forceinline__ int block_item(const AttnArgs& a, int* s_item, int wv
 // per CU, one wave of each per SIMD).
 template <int NW, int DP>
 struct FastOccupancy {
-  static constexpr bool SMALL_GRID = NW == 4 && DP <= 64;
-  static constexpr int WAVES_PER_EU = NW > 8 ? 3 : (NW > 4 ? 2 : (SMALL_GRID ? 4 : 1));
+  static constexpr bool SMALL_GRID = NW == 4 && DP <= 128;
+  static constexpr int WAVES_PER_EU = NW > 8 ? 3 : (NW > 4 ? 2 : (SMALL_GRID ? (DP <= 64 ? 4 : 2) : 1));
 };
 
 template <typename E, int DP, int NW, bool FUSED, bool PARTIAL>
@@ -1562,12 +1562,15 @@ FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")
 // kernel and each SIMD's four waves from four workgroups. Chosen by the launch when the 8-wave
 // kernel's items would fill at most a few rounds of its resident workgroups: the reference
 // harness's Hq4/Hkv2 shape at 8K and 32K measured 11% and 4.4% faster, a grid of eight rounds
-// (B1 Hq32/Hkv8 N32768) 3% slower.
+// (B1 Hq32/Hkv8 N32768) 3% slower. At tile dims 96 and 128 (two workgroups per CU) it stands in
+// for attn_rt2_kernel below one round of the latter's items (B2 Hq8/Hkv2 N4000: 30% faster).
 #define FE_FAST_SMALL_DIM(E, e, DP) \
   fast_entry<E, DP, 4, false, false>("attn_fast4<" e "," #DP ">"), fast_entry<E, DP, 4, false, true>("attn_fast4<" e "," #DP ",partial>")
-// [dtype][tile dim 32, 64][partial]
+// [dtype][tile dim 32, 64, 96, 128][partial]
 FusedPlan g_fast_small[] = {FE_FAST_SMALL_DIM(F16, "f16", 32), FE_FAST_SMALL_DIM(F16, "f16", 64),
-                            FE_FAST_SMALL_DIM(BF16, "bf16", 32), FE_FAST_SMALL_DIM(BF16, "bf16", 64)};
+                            FE_FAST_SMALL_DIM(F16, "f16", 96), FE_FAST_SMALL_DIM(F16, "f16", 128),
+                            FE_FAST_SMALL_DIM(BF16, "bf16", 32), FE_FAST_SMALL_DIM(BF16, "bf16", 64),
+                            FE_FAST_SMALL_DIM(BF16, "bf16", 96), FE_FAST_SMALL_DIM(BF16, "bf16", 128)};
 // Attention-only traversal with two row tiles per wave at tile dims 96 and 128 (attn_rt2_kernel:
 // 8 waves, 16 row tiles per workgroup), head dims below the tile dim included: 3-5% faster than
 // fused_fast_kernel's 12 waves of one row tile on every measured configuration at D = 128, 3% at
@@ -1625,9 +1628,9 @@ bool fast_plan(const AttnArgs& a, int dtype, FusedPlan& plan) {
 
 bool fast_plan_small(const AttnArgs& a, int dtype, FusedPlan& plan) {
   const int slot = fast_slot(a.D);
-  if (slot < 0 || slot > 1 || !(a.abs_scale_log2 > 0.f) || !fast_layout(a) || (a.score && !a.bias)) return false;
+  if (slot < 0 || slot > 3 || !(a.abs_scale_log2 > 0.f) || !fast_layout(a) || (a.score && !a.bias)) return false;
   const int partial = (a.D != 32 * (slot + 1) || a.Dq != 32 * (slot + 1)) ? 1 : 0;
-  plan = g_fast_small[2 * (2 * (dtype == 1 ? 1 : 0) + slot) + partial];
+  plan = g_fast_small[2 * (4 * (dtype == 1 ? 1 : 0) + slot) + partial];
   return true;
 }
 

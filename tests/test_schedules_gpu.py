@@ -156,13 +156,38 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     assert ((i_small - i_big[:1]).abs() <= 2e-6 * i_big[:1].abs() + 1e-6 * scale).all()
 
 
+@pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (120, torch.float16), (96, torch.bfloat16)])
+def test_small_grid_kernel_at_tile_dims_96_and_128(d, dtype):
+    """Tile dims 96 and 128 run the 4-wave small-grid attention kernel instead of the two-row-tile
+    kernel when the latter's 16-row-tile items would not fill one round of its workgroups (one
+    per CU). It computes every row tile as the fused single kernel does (one row tile per wave,
+    reference max over the first 64 keys): output bitwise equal to fe_prefill's, importance up to
+    FP32 atomic order."""
+    b, hq, hk, n = 1, 8, 2, 3000
+    print(f"small-grid attention kernel d={d} {dtype} b={b} hq={hq} hk={hk} n={n}", flush=True)
+    q = seeded_randn((b, hq, n, d), dtype, 23 + d)
+    k = seeded_randn((b, hk, n, d), dtype, 24 + d)
+    v = seeded_randn((b, hk, n, d), dtype, 25 + d)
+    o_ws, i_ws = _run(q, k, v, True, True, 0.0, 0, use_ws=True)
+    plan = _last_plan()
+    tile = (d + 31) // 32 * 32
+    e = "bf16" if dtype == torch.bfloat16 else "f16"
+    part = "" if d == tile else ",partial"
+    assert plan == "attn_fast4<%s,%d%s> + replay_fast<%s,%d%s>" % (e, tile, part, e, tile, part), plan
+    o_fu, i_fu = _run(q, k, v, True, True, 0.0, 0, use_ws=False)
+    assert torch.equal(o_ws, o_fu)
+    assert float((i_ws - i_fu).abs().max()) <= 3e-6 * float(i_fu.abs().max())
+
+
 @pytest.mark.parametrize("b,hq,hk,n,d,dtype,causal,decay,window", [
+    # (launches of more than one round of the two-row-tile kernel's items, below which the
+    # small-grid kernel runs instead)
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.1, 0),       # llama8k's schedule: 1050 rows replayed
-    (2, 8, 2, 3000, 120, torch.float16, True, 0.0, 200),      # partial tile dim, ragged N, fp16
-    (1, 16, 2, 2048, 96, torch.bfloat16, False, 0.0, 100),    # tile dim 96, non-causal
+    (2, 8, 2, 9000, 120, torch.float16, True, 0.0, 200),      # partial tile dim, ragged N, fp16
+    (1, 16, 2, 8320, 96, torch.bfloat16, False, 0.0, 100),    # tile dim 96, non-causal
     # every row replayed: the heaviest row groups as items, the replay kernel for the others
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.0, 0),
-    (2, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
+    (3, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
 ])
 def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, decay, window):
     """Short observation windows on the two-row-tile attention kernel run the replay as work
