@@ -2,8 +2,9 @@
 
 Each case draws its shape and options from a seeded generator: batch, KV heads and GQA group
 (1, 2, 4 or 7), N from 1 to 700 (tile edges included), head dims 16..256 (the fast kernels for
-multiples of 8 up to 256, on full and partial tiles, with the two-row-tile attention kernel at
-72..128; the generic kernel for 100), fp16/bf16, causal or not, softmax scale (default, small,
+multiples of 8 up to 256, on full and partial tiles; at these sizes every launch is below one
+round of the two-row-tile kernel's work items, so 72..128 run the small-grid kernel; the generic
+kernel for 100), fp16/bf16, causal or not, softmax scale (default, small,
 negative), recency decay
 (including decays large enough that the replay keeps only a few rows), observation window,
 value weighting, contiguous or transposed layouts, and a selection budget, reserved suffix and
