@@ -705,6 +705,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_REPLAY_ITEMS_PER_WG
 #define FE_REPLAY_ITEMS_PER_WG 2
 #endif
+#ifndef FE_REPLAY_ITEMS_FAST
+#define FE_REPLAY_ITEMS_FAST 1
+#endif
 #ifndef FE_TAIL_REPLAY_FRAC
 #define FE_TAIL_REPLAY_FRAC 0.03
 #endif
@@ -903,8 +906,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     set_error(std::string("fe_prefill: hipFuncSetAttribute: ") + hipGetErrorString(err));
     return FE_ERR_HIP;
   }
+  int64_t resident = 0;
   if (ctr) {
-    int64_t resident = 0;
     if ((err = resident_blocks(plan.fn, 64 * plan.waves, plan.lds, stream, &resident)) != hipSuccess) {
       set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
       return FE_ERR_HIP;
@@ -930,9 +933,17 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // eight key tiles where the keys allow (a window of 128 rows at N = 32K otherwise made items of
   // two tiles, 0.4% slower overall).
   bool replay_items = false;
-  if (FE_REPLAY_ITEMS && split && ctr && plan.rows == 16 && items <= kMaxDoneItems &&
+  // Replay items run on the two-row-tile kernel and on fused_fast_kernel at tile dims 32 and 64
+  // (FE_REPLAY_ITEMS_FAST; D = 32 and 64 short windows and the reference harness's shape at 32K
+  // 2-3.5% faster, tile dim 256 7.5% slower), in launches whose attention items fill every resident
+  // workgroup: a smaller launch runs one workgroup per item, so its replay items would queue
+  // behind the attention items on those workgroups while the replay kernel spreads over the whole
+  // chip (the reference harness's shape at 8K: 5.8% slower).
+  const bool item_plan = fast && (plan.rows == 16 || (FE_REPLAY_ITEMS_FAST && plan.rows <= 8 && D <= 64)) &&
+                         items >= resident;
+  if (FE_REPLAY_ITEMS && split && ctr && item_plan && items <= kMaxDoneItems &&
       (double)(N - a.win_lo) <= FE_REPLAY_ITEMS_MAX * (double)N) {
-    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / 16;
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
     const int64_t max_tiles = (N + 63) / 64;
     const int64_t rs_max = (max_tiles + 7) / 8;
@@ -951,12 +962,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // items are the first taken, so the biases are ready when they start); the replay kernel
   // replays the rows below them (every row replayed: 0.2-1.4% faster pairs; 6% was slower).
   int64_t tail_groups = 0;
-  if (FE_TAIL_REPLAY_FRAC > 0.0 && !replay_items && FE_REPLAY_ITEMS && split && ctr && plan.rows == 16 &&
-      items <= kMaxDoneItems && 16 % rplan.rows == 0) {
-    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / 16;
+  if (FE_TAIL_REPLAY_FRAC > 0.0 && !replay_items && FE_REPLAY_ITEMS && split && ctr && item_plan &&
+      items <= kMaxDoneItems) {
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
+    const int64_t ng_max = (int64_t)a.wg_bh - wg_lo - 1;
     int64_t ng = (int64_t)ceil(FE_TAIL_REPLAY_FRAC * (double)((int64_t)a.wg_bh - wg_lo));
-    if (ng > (int64_t)a.wg_bh - wg_lo - 1) ng = (int64_t)a.wg_bh - wg_lo - 1;
-    if (ng > 0) {
+    // the replay kernel's rows end on a boundary of its own row groups
+    while (ng < ng_max && (((int64_t)a.wg_bh - ng) * plan.rows) % rplan.rows != 0) ++ng;
+    if (ng > 0 && ng <= ng_max && (((int64_t)a.wg_bh - ng) * plan.rows) % rplan.rows == 0) {
       const int64_t nwg = B * Hkv * ng;
       const int64_t max_tiles = (N + 63) / 64;
       const int64_t rs_max = (max_tiles + 7) / 8;
@@ -1036,7 +1049,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     // (tiles before query block win_lo/32 have none), heaviest first; with tail groups, only
     // the row tiles below them.
     AttnArgs r = a;
-    r.wg_bh = tail_groups ? (int)((((int64_t)a.wg_bh - tail_groups) * 16) / rplan.rows)
+    r.wg_bh = tail_groups ? (int)((((int64_t)a.wg_bh - tail_groups) * plan.rows) / rplan.rows)
                           : (int)((tiles_bh + rplan.rows - 1) / rplan.rows);
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / rplan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)r.wg_bh - wg_lo);

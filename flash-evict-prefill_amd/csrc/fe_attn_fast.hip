@@ -265,6 +265,34 @@ __device__ __forceinline__ int block_item(const AttnArgs& a, int* s_item, int wv
   return __builtin_amdgcn_readfirstlane(*s_item);
 }
 
+// Replay items of the attention kernels: lane 0 of the calling wave waits
+// until attention item `dep` has published its rows' replay biases (its bit in a.done) and
+// returns whether it has. The bias words are written and read as agent-scope relaxed atomics
+// (write-through stores and loads that bypass a stale L2 line), the writer waits for its stores
+// before its workgroup sets the bit, and the waiting lane's load of the bit completes before the
+// workgroup barrier that precedes the bias loads, so a bias read after the bit is seen is the
+// one written. Attention items are numbered before replay items in every queue and the window
+// rows a replay item needs are the heaviest attention items, taken first, so the wait is short;
+// it is bounded by about 17 us per key tile of the dependency (five times what a tile takes;
+// a.wait_base + a.wait_per_tile polls of about 0.27 us),
+// and when it runs out (the dependency's workgroup not resident, say, on a GPU another kernel
+// shares) the caller computes the dependency itself: an attention item writes the same output
+// and biases whoever runs it.
+__device__ __forceinline__ bool wait_item_done(const AttnArgs& a, int dep, int dep_tiles) {
+  bool ok = true;
+  if (lane_now() == 0) {
+    const unsigned bit = 1u << (dep & 31);
+    unsigned* w = a.done + (dep >> 5);
+    const int polls = a.wait_base + a.wait_per_tile * dep_tiles;
+    ok = false;
+    for (int spin = 0; spin < polls && !ok; ++spin) {
+      ok = (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & bit) != 0;
+      if (!ok) __builtin_amdgcn_s_sleep(8);
+    }
+  }
+  return ok;
+}
+
 // NW waves of one row tile each (8: two waves per SIMD; 12: three, at D = 128, which then
 // reads K fragments in two halves and V fragments without prefetch to fit 168 registers). FUSED adds the replay traversal (fe_prefill without a
 // workspace); otherwise the kernel hands each row's replay bias to replay_fast_kernel.
@@ -306,7 +334,7 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
   const bool dmaw = wv < 4;                      // waves 0-3 issue the tile DMA
   const int N = a.N;
 
-  __shared__ int s_item;
+  __shared__ int s_item, s_ready;
   // One work item; `return` ends it.
   auto run_item = [&](const int item) __attribute__((always_inline)) {
     const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
@@ -638,12 +666,25 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
     // ---------------- traversal 2: replay
     if (!a.score) return;
     if (a.bias) {
-      // Split schedule: hand the row's replay bias (see below) to replay_fast_kernel.
+      // Split schedule: hand the row's replay bias (see below) to replay_fast_kernel, or to the
+      // replay items of this launch (agent-scope atomic store; after every wave's stores, one
+      // lane sets the item's bit)
       const int qi = q0 + l32;
+      const bool items = NW <= 8 && a.nattn < a.nitems;  // the launch makes none for 12 waves
       if (hh == 0 && tv && qi < N) {
         const bool live = qi >= a.win_lo;
-        a.bias[(long long)(b * a.Hq + head) * N + qi] =
-            live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+        const float bv = live ? (m_run + fast_log2(l_tot) - a.decay_log2 * (float)(qi - (N - 1))) : POS_INF;
+        float* bp = a.bias + (long long)(b * a.Hq + head) * N + qi;
+        if (items)
+          __hip_atomic_store(bp, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *bp = bv;
+      }
+      if (items && wg_q_hi - 1 >= a.win_lo) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (wv == 0 && lane_now() == 0)
+          __hip_atomic_fetch_or(a.done + (item >> 5), 1u << (item & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       return;
     }
@@ -746,44 +787,157 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
       flush((ntiles - 1) * BN, (ntiles - 1) & 1);
     }
   };
+  // One replay item (split schedule with replay items; reference flash_evict/prefill.py:61-83):
+  // the window rows of one attention item's NW row tiles (one per wave) against one key range,
+  // the arithmetic of replay_fast_kernel with one row tile per wave: S = Q K^T with lanes holding
+  // keys, exp2(s * scale*log2e - b_q) summed over the rows of each key in-lane and over the waves
+  // in LDS (the V buffers, unused here), one FP32 atomic per key and tile. It first waits for
+  // the attention item of its rows (same decode) to publish their biases, or runs that item.
+  auto run_replay = [&](const int ritem) __attribute__((always_inline)) {
+    const int lane = lane_now(), l32 = lane & 31, hh = lane >> 5;
+    int BH = a.BH, G = a.G, Hkv = a.Hkv, rsplit = a.rsplit;
+    asm volatile("" : "+s"(BH), "+s"(G), "+s"(Hkv), "+s"(rsplit));
+    const int bh = (int)((unsigned)ritem % (unsigned)BH);
+    const int rest = (int)((unsigned)ritem / (unsigned)BH);
+    const int ks = rest % rsplit;
+    const int wg = a.wg_bh - 1 - rest / rsplit;
+    const int b = bh / Hkv, hkv = bh - b * Hkv;
+    const int t_begin = wg * NW;
+    const int t_end = min(a.tiles_bh, t_begin + NW);
+    const int kv_end = a.causal ? min(N, ((t_end - 1) / G + 1) * 32) : N;
+    const int ntiles_all = (kv_end + BN - 1) / BN;
+    const int per = (ntiles_all + rsplit - 1) / rsplit;
+    const int it_lo = ks * per, it_hi = min(ntiles_all, it_lo + per);
+    const int dep = (a.wg_bh - 1 - wg) * BH + bh;
+    if (wv == 0) {
+      const bool ok = wait_item_done(a, dep, ntiles_all);
+      if (lane_now() == 0) s_ready = ok ? 1 : 0;
+    }
+    __syncthreads();
+    if (!__builtin_amdgcn_readfirstlane(s_ready)) {
+      run_item(dep);
+      __syncthreads();
+    }
+    if (it_lo >= it_hi) return;
+
+    // this wave's row tile; nb: minus the biases of the 16 rows a lane holds (register i:
+    // row 8(i/4) + 4h + i%4)
+    const int t = t_begin + wv;
+    const bool tv = t < t_end;
+    const int tt = tv ? t : t_begin;
+    const int q0 = (tt / G) * 32;
+    const int head = hkv * G + (tt - (tt / G) * G);
+    const bool rin = tv && q0 + 31 >= a.win_lo;
+    const int wave_hi_r = rin ? (a.causal ? min(q0 + 31, N - 1) : N - 1) : -1;
+    const u32 qneg = a.neg_scale ? 0x80008000u : 0u;
+    u32x4 qf[NDC];
+    float nb[16];
+    {
+      const int qr = q0 + l32;
+      const bool ok = rin && qr < N;
+      const u16* qp = a.q + b * a.qs[0] + head * a.qs[1] + (long long)(ok ? qr : 0) * a.qs[2];
+  #pragma unroll
+      for (int c = 0; c < NDC; ++c)
+        qf[c] = ok ? ((load8(qp, a.qs[3], 16 * c + 8 * hh, PARTIAL ? a.Dq : DP, a.qvec) & a.qmask) ^ qneg)
+                   : (u32x4){0u, 0u, 0u, 0u};
+      const float br = ok ? __hip_atomic_load(a.bias + (long long)(b * a.Hq + head) * N + qr, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : POS_INF;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) nb[i] = -__shfl(br, 8 * (i >> 2) + 4 * hh + (i & 3));
+    }
+    const u32 koff = (u32)(l32 * 32 + ((hh ^ ((l32 >> 3) & 1)) << 4));
+    const u32 krow = (u32)(a.ks[2] * 2);
+    const unsigned char* kg = (const unsigned char*)(a.k + b * a.ks[0] + hkv * a.ks[1]);
+    float* imp_row = a.imp + (long long)bh * N;
+    float* red_r = (float*)lds_v0;                 // [2][NW][BN] per-wave column sums
+    auto r_dma = [&](int kb, unsigned char* ldst) {
+      const int ln = lane_now();
+      const u32 sw = (u32)((ln & 1) ^ ((ln >> 4) & 1));
+      dma_tile_cm<DPW, 32, PARTIAL>(kg, krow, (u32)(ln >> 1) * krow + (sw << 4), kb, N, ldst, wv, a.D, sw << 3);
+    };
+    auto r_flush = [&](int kb_prev, int buf_prev) {
+      if (wv == 0) {
+        const int ln = lane_now();
+        const float* rr = red_r + buf_prev * NW * BN + ln;
+        float sum = 0.f;
+  #pragma unroll
+        for (int w = 0; w < NW; w += 2) sum += rr[w * BN] + rr[(w + 1) * BN];
+        const int key = kb_prev + ln;
+        if (sum != 0.f && key < N) unsafeAtomicAdd(imp_row + key, sum);
+      }
+    };
+    auto r_step = [&](int it, int BUF) __attribute__((always_inline)) {
+      const int kb = it * BN;
+      if (dmaw) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (it > it_lo) r_flush(kb - BN, BUF ^ 1);
+      if (dmaw && it + 1 < it_hi) r_dma(kb + BN, BUF == 0 ? lds_k1 : lds_k0);
+      float cs[2] = {0.f, 0.f};
+      if (kb <= wave_hi_r) {
+        const unsigned char* kt = BUF == 0 ? lds_k0 : lds_k1;
+  #pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          f32x16 sacc = (f32x16){};
+  #pragma unroll
+          for (int c = 0; c < NDC; ++c) {
+            const u32x4 kf = *(const u32x4*)(kt + c * 2048 + s * 1024 + koff);
+            sacc = E::mfma(qf[c], kf, sacc);
+          }
+          // lanes hold key kb + 32s + l32; causal mask on diagonal halves
+          if (a.causal && kb + 32 * s + 31 > q0) {
+            const int rel = kb + 32 * s + l32 - q0 - 4 * hh;
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[i] = rel > 8 * (i >> 2) + (i & 3) ? NEG_INF : sacc[i];
+          }
+          float c4[4];
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float e = fast_exp2(fmaf(sacc[i], a.abs_scale_log2, nb[i]));
+            if (i < 4)
+              c4[i] = e;
+            else
+              c4[i & 3] += e;
+          }
+          cs[s] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+        }
+      }
+      cs[0] = half_swap_sum(cs[0]);
+      cs[1] = half_swap_sum(cs[1]);
+      if (hh == 0) {
+        float* rb = red_r + BUF * NW * BN + wv * BN;
+        rb[l32] = cs[0];
+        rb[32 + l32] = cs[1];
+      }
+    };
+    if (dmaw) r_dma(it_lo * BN, lds_k0);
+    for (int it = it_lo; it < it_hi; it += 2) {
+      r_step(it, 0);
+      if (it + 1 < it_hi) r_step(it + 1, 1);
+    }
+    __syncthreads();
+    r_flush((it_hi - 1) * BN, (it_hi - 1 - it_lo) & 1);
+  };
+
   if constexpr (FUSED) {
     // the kernel with the replay traversal (no workspace, so no queue) runs one item
     run_item((int)blockIdx.x);
   } else {
     const int item_end = a.queue ? a.nitems : (int)blockIdx.x + 1;
-    for (int item = (int)blockIdx.x; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end)
-      run_item(item);
-  }
-}
-
-
-// Replay items of attn_rt2_kernel (short observation windows): lane 0 of the calling wave waits
-// until attention item `dep` has published its rows' replay biases (its bit in a.done) and
-// returns whether it has. The bias words are written and read as agent-scope relaxed atomics
-// (write-through stores and loads that bypass a stale L2 line), the writer waits for its stores
-// before its workgroup sets the bit, and the waiting lane's load of the bit completes before the
-// workgroup barrier that precedes the bias loads, so a bias read after the bit is seen is the
-// one written. Attention items are numbered before replay items in every queue and the window
-// rows a replay item needs are the heaviest attention items, taken first, so the wait is short;
-// it is bounded by about 17 us per key tile of the dependency (five times what a tile takes;
-// a.wait_base + a.wait_per_tile polls of about 0.27 us),
-// and when it runs out (the dependency's workgroup not resident, say, on a GPU another kernel
-// shares) the caller computes the dependency itself: an attention item writes the same output
-// and biases whoever runs it.
-__device__ __forceinline__ bool wait_item_done(const AttnArgs& a, int dep, int dep_tiles) {
-  bool ok = true;
-  if (lane_now() == 0) {
-    const unsigned bit = 1u << (dep & 31);
-    unsigned* w = a.done + (dep >> 5);
-    const int polls = a.wait_base + a.wait_per_tile * dep_tiles;
-    ok = false;
-    for (int spin = 0; spin < polls && !ok; ++spin) {
-      ok = (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & bit) != 0;
-      if (!ok) __builtin_amdgcn_s_sleep(8);
+    for (int item = (int)blockIdx.x; item < item_end; item = a.queue ? next_item(a, &s_item, wv) : item_end) {
+      if constexpr (NW <= 8) {
+        if (item < a.nattn)
+          run_item(item);
+        else
+          run_replay(item - a.nattn);
+      } else {
+        run_item(item);                            // no replay items (the launch does not make any)
+      }
     }
   }
-  return ok;
 }
+
+
 
 // Traversal 1 (reference flash_evict/prefill.py:37-60) with two row tiles per wave (attention
 // only: the split schedule, or no importance), tile dims 96 and 128. Eight waves, two per SIMD, each holding the Q fragments

@@ -93,9 +93,9 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  *     computed the same way whichever workgroup takes it: the output is bitwise that of the
  *     static schedule, the importance equal up to FP32 atomic order;
  *   * with the whole workspace and a short observation window (at most a quarter of the rows
- *     replayed) at head dims 72..128, the replay runs as work items of the attention launch
- *     instead of a second kernel (same arithmetic: output bitwise equal, importance equal up
- *     to FP32 atomic order); each waits for its rows' attention item, and runs that item
+ *     replayed) at head dims 8..64 and 72..128, in launches that fill the GPU, the replay runs
+ *     as work items of the attention launch instead of a second kernel (same arithmetic:
+ *     output bitwise equal, importance equal up to FP32 atomic order); each waits for its rows' attention item, and runs that item
  *     itself if the wait runs out (a GPU another kernel shares). With longer windows the
  *     heaviest 3% of the row groups replay that way, in the attention launch's tail, and the
  *     second kernel replays the other rows;

@@ -149,8 +149,10 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     small_plan = _last_plan()
     o_big, i_big = _run(q, k, v, True, True, 0.0, 0, use_ws=True)
     big_plan = _last_plan()
+    # every row replayed: in the launch whose attention items fill every resident workgroup, the
+    # heaviest row groups' replay runs as items of the attention launch
     assert small_plan == "attn_fast4<bf16,%d> + replay_fast<bf16,%d>" % (d, d), small_plan
-    assert big_plan == "attn_fast<bf16,%d> + replay_fast<bf16,%d>" % (d, d), big_plan
+    assert big_plan == "attn_fast<bf16,%d> with replay items + replay_fast<bf16,%d>" % (d, d), big_plan
     assert torch.equal(o_small, o_big[:1])
     scale = i_big[:1].abs().amax(dim=-1, keepdim=True)
     assert ((i_small - i_big[:1]).abs() <= 2e-6 * i_big[:1].abs() + 1e-6 * scale).all()
@@ -188,12 +190,18 @@ def test_small_grid_kernel_at_tile_dims_96_and_128(d, dtype):
     # every row replayed: the heaviest row groups as items, the replay kernel for the others
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.0, 0),
     (3, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
+    # the one-row-tile kernel (fused_fast_kernel) at tile dims 32 and 64: 8 waves, the 4-wave
+    # small grid (launches whose attention items fill every resident workgroup)
+    (1, 32, 8, 8192, 64, torch.bfloat16, True, 0.1, 0),
+    (1, 4, 2, 32768, 64, torch.float16, True, 0.0, 0),
+    (1, 32, 8, 16384, 32, torch.bfloat16, False, 0.0, 300),
+    (1, 16, 4, 8192, 56, torch.float16, True, 0.0, 100),
 ])
 def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, decay, window):
-    """Short observation windows on the two-row-tile attention kernel run the replay as work
-    items of the attention launch (the whole workspace); longer ones run the heaviest row groups'
-    replay as items and the others on the replay kernel; a workspace of the replay biases alone
-    runs the separate replay kernel for every row. Same attention items and the same replay
+    """Short observation windows run the replay as work items of the attention launch (the whole
+    workspace), on both fast attention kernels; longer ones run the heaviest row groups' replay
+    as items and the others on the replay kernel; a workspace of the replay biases alone runs the
+    separate replay kernel for every row. Same attention items and the same replay
     arithmetic: the output is bitwise equal and the importance equal up to FP32 atomic order.
     fe_last_plan names the schedule each launch ran."""
     print(f"replay items vs replay kernel b={b} hq={hq} hk={hk} n={n} d={d} {dtype} causal={causal} "
@@ -207,22 +215,22 @@ def test_replay_items_match_the_replay_kernel(b, hq, hk, n, d, dtype, causal, de
     plan_rk = _last_plan()
     # at most a quarter of the rows replayed (fe_replay_rows): all of them as items
     short = 4 * _lib.lib().fe_replay_rows(n, min(n, window or n), decay) <= n
-    assert plan_it.startswith("attn_rt2<") and " with replay items" in plan_it, plan_it
+    assert " with replay items" in plan_it, plan_it
     assert plan_it.endswith(" with replay items") == short, plan_it
     assert " + replay_fast<" in plan_rk and " with replay items" not in plan_rk, plan_rk
     assert torch.equal(o_it, o_rk)
     assert float((i_it - i_rk).abs().max()) <= 3e-6 * float(i_rk.abs().max())
 
 
-@pytest.mark.parametrize("decay", [0.1, 0.0])
-def test_replay_item_runs_its_dependency_when_the_wait_runs_out(monkeypatch, decay):
+@pytest.mark.parametrize("d,decay", [(128, 0.1), (128, 0.0), (64, 0.1), (64, 0.0)])
+def test_replay_item_runs_its_dependency_when_the_wait_runs_out(monkeypatch, d, decay):
     """A replay item whose attention item has not published its biases within the wait's bound
     runs that attention item itself (attention items are idempotent: whoever runs one writes the
     same output and biases). FLASH_EVICT_REPLAY_WAIT=0 makes every replay item take that path at
     once; the results equal the replay kernel's (bitwise output, importance up to FP32 atomic
     order). Decay 0.1: every replayed row as items; decay 0: the heaviest row groups as items,
     the others on the replay kernel."""
-    b, hq, hk, n, d = 1, 32, 8, 8192, 128
+    b, hq, hk, n = 1, 32, 8, 8192
     print(f"replay items running their dependencies b={b} hq={hq} hk={hk} n={n} d={d} decay={decay}", flush=True)
     q = seeded_randn((b, hq, n, d), torch.bfloat16, 71)
     k = seeded_randn((b, hk, n, d), torch.bfloat16, 72)
