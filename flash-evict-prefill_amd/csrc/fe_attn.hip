@@ -1061,14 +1061,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     r.rsplit = (int)rs;
     int64_t rgrid = nwg * rs;
     if (ctr) {
-      int64_t resident = 0;
-      if ((err = resident_blocks(rplan.fn, 64 * rplan.waves, 0, stream, &resident)) != hipSuccess) {
+      int64_t rresident = 0;
+      if ((err = resident_blocks(rplan.fn, 64 * rplan.waves, 0, stream, &rresident)) != hipSuccess) {
         set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
         return FE_ERR_HIP;
       }
       r.queue = ctr + kQueueReplay;
       r.nitems = (int)rgrid;
-      r.nstatic = (int)(rgrid < resident ? rgrid : resident);
+      r.nstatic = (int)(rgrid < rresident ? rgrid : rresident);
       const int64_t rrows = rplan.rows, rwgb = r.wg_bh;
       r.tail = (int)tail_start(rgrid / (B * Hkv), B * Hkv, r.nstatic, FE_TAIL_REPLAY, [&](int64_t g) {
         const int64_t ks = g % rs, wg = rwgb - 1 - g / rs;
