@@ -705,6 +705,10 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_REPLAY_ITEMS_PER_WG
 #define FE_REPLAY_ITEMS_PER_WG 2
 #endif
+// Key tiles a replay item holds at least (where the rows' keys allow).
+#ifndef FE_REPLAY_ITEM_MIN_TILES
+#define FE_REPLAY_ITEM_MIN_TILES 8
+#endif
 #ifndef FE_REPLAY_ITEMS_FAST
 #define FE_REPLAY_ITEMS_FAST 1
 #endif
@@ -946,7 +950,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
     const int64_t max_tiles = (N + 63) / 64;
-    const int64_t rs_max = (max_tiles + 7) / 8;
+    const int64_t rs_max = (max_tiles + FE_REPLAY_ITEM_MIN_TILES - 1) / FE_REPLAY_ITEM_MIN_TILES;
     int64_t rs = (FE_REPLAY_ITEMS_PER_WG * (int64_t)a.nstatic + nwg - 1) / nwg;
     rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
     if (items + nwg * rs < (int64_t)0x7fffffff) {
@@ -972,7 +976,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     if (ng > 0 && ng <= ng_max && (((int64_t)a.wg_bh - ng) * plan.rows) % rplan.rows == 0) {
       const int64_t nwg = B * Hkv * ng;
       const int64_t max_tiles = (N + 63) / 64;
-      const int64_t rs_max = (max_tiles + 7) / 8;
+      const int64_t rs_max = (max_tiles + FE_REPLAY_ITEM_MIN_TILES - 1) / FE_REPLAY_ITEM_MIN_TILES;
       int64_t rs = (FE_REPLAY_ITEMS_PER_WG * (int64_t)a.nstatic + nwg - 1) / nwg;
       rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
       if (items + nwg * rs < (int64_t)0x7fffffff) {
