@@ -34,7 +34,8 @@ struct AttnArgs {
   int nitems;                       // dynamic schedule: work items of the launch
   int nstatic;                      // dynamic schedule: workgroups launched (each starts with item blockIdx.x)
   int tail;                         // dynamic schedule: first item of the queues' light parts (nitems: none)
-  int nattn;                        // attention items; items past them are replay items (attn_rt2_kernel)
+  int nattn;                        // attention items; items past them are replay items
+  int rwg0;                         // replay items in ascending row groups from rwg0 (-1: heaviest first)
   unsigned* done;                   // replay items: one bit per attention item, set once its biases are out
   int wait_base, wait_per_tile;     // replay items: polls of a dependency's bit (plus per key tile) before running it
   int qvec, kvec, vvec, ovec;       // 16-byte (q/k/v) and 8-byte (out) vector access allowed

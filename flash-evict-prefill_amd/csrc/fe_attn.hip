@@ -706,6 +706,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #define FE_REPLAY_ITEMS_PER_WG 2
 #endif
 // Key tiles a replay item holds at least (where the rows' keys allow).
+#ifndef FE_SMALL_LAUNCH_ITEMS
+#define FE_SMALL_LAUNCH_ITEMS 1
+#endif
 #ifndef FE_REPLAY_ITEM_MIN_TILES
 #define FE_REPLAY_ITEM_MIN_TILES 8
 #endif
@@ -805,6 +808,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   a.nstatic = 0;
   a.tail = 0;
   a.nattn = 0x7fffffff;
+  a.rwg0 = -1;
   a.done = nullptr;
   // Polls of a replay item's dependency before it runs the attention item itself: 4096 plus 64
   // per key tile (each poll sleeps about 0.27 us). FLASH_EVICT_REPLAY_WAIT=0 makes every replay
@@ -937,6 +941,32 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // eight key tiles where the keys allow (a window of 128 rows at N = 32K otherwise made items of
   // two tiles, 0.4% slower overall).
   bool replay_items = false;
+  // Causal launches at tile dims 32 and 64 whose attention items do not fill the resident
+  // workgroups: a grid of every resident workgroup, and all the replay as items in ascending row
+  // groups, so the light rows' replay (their attention items end first) runs beside the heaviest
+  // attention items on CUs that would idle, and the replay kernel's launch after the heaviest
+  // item goes (the reference harness's shape at 8K: 8% faster). Without the causal mask every
+  // attention item ends at once (B2 Hq8/Hkv2 N4000 D128 non-causal: 13% slower).
+  if (FE_REPLAY_ITEMS && FE_SMALL_LAUNCH_ITEMS && split && ctr && fast && causal && D <= 64 && plan.rows <= 8 &&
+      items < resident && items <= kMaxDoneItems) {
+    const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
+    const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
+    const int64_t max_tiles = (N + 63) / 64;
+    const int64_t rs_max = (max_tiles + FE_REPLAY_ITEM_MIN_TILES - 1) / FE_REPLAY_ITEM_MIN_TILES;
+    int64_t rs = nwg > 0 ? (FE_REPLAY_ITEMS_PER_WG * resident + nwg - 1) / nwg : 1;
+    rs = rs < 1 ? 1 : (rs > rs_max ? rs_max : rs);
+    if (nwg > 0 && items + nwg * rs < (int64_t)0x7fffffff) {
+      replay_items = true;
+      a.nattn = (int)items;
+      a.nitems = (int)(items + nwg * rs);
+      a.rsplit = (int)rs;
+      a.rwg0 = (int)wg_lo;
+      a.done = (unsigned*)(ctr + kQueueDone);
+      a.nstatic = (int)((int64_t)a.nitems < resident ? (int64_t)a.nitems : resident);
+      if (a.tail < a.nstatic) a.tail = a.nstatic;
+      grid = a.nstatic;
+    }
+  }
   // Replay items run on the two-row-tile kernel and on fused_fast_kernel at tile dims 32 and 64
   // (FE_REPLAY_ITEMS_FAST; D = 32 and 64 short windows and the reference harness's shape at 32K
   // 2-3.5% faster, tile dim 256 7.5% slower), in launches whose attention items fill every resident
@@ -945,7 +975,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // chip (the reference harness's shape at 8K: 5.8% slower).
   const bool item_plan = fast && (plan.rows == 16 || (FE_REPLAY_ITEMS_FAST && plan.rows <= 8 && D <= 64)) &&
                          items >= resident;
-  if (FE_REPLAY_ITEMS && split && ctr && item_plan && items <= kMaxDoneItems &&
+  if (FE_REPLAY_ITEMS && !replay_items && split && ctr && item_plan && items <= kMaxDoneItems &&
       (double)(N - a.win_lo) <= FE_REPLAY_ITEMS_MAX * (double)N) {
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
@@ -1034,6 +1064,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
       (void)hipGetLastError();
       replay_items = false;
       tail_groups = 0;
+      a.rwg0 = -1;
       a.nattn = 0x7fffffff;
       a.nitems = (int)items;
       a.rsplit = 1;

@@ -800,7 +800,7 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
     const int bh = (int)((unsigned)ritem % (unsigned)BH);
     const int rest = (int)((unsigned)ritem / (unsigned)BH);
     const int ks = rest % rsplit;
-    const int wg = a.wg_bh - 1 - rest / rsplit;
+    const int wg = a.rwg0 >= 0 ? a.rwg0 + rest / rsplit : a.wg_bh - 1 - rest / rsplit;
     const int b = bh / Hkv, hkv = bh - b * Hkv;
     const int t_begin = wg * NW;
     const int t_end = min(a.tiles_bh, t_begin + NW);
@@ -1328,7 +1328,7 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       const int bh = (int)((unsigned)ritem % (unsigned)BH);
       const int rest = (int)((unsigned)ritem / (unsigned)BH);
       const int ks = rest % rsplit;
-      const int wg = a.wg_bh - 1 - rest / rsplit;
+      const int wg = a.rwg0 >= 0 ? a.rwg0 + rest / rsplit : a.wg_bh - 1 - rest / rsplit;
       const int b = bh / Hkv, hkv = bh - b * Hkv;
       const int t_begin = wg * (NW * RT);
       const int t_end = min(a.tiles_bh, t_begin + NW * RT);

@@ -89,7 +89,8 @@ def test_replay_scales_bf16(d, scale, decay):
     out, imp = prefill(q, k, v, scale=scale, recency_decay=decay)
     tile = (d + 31) // 32 * 32
     plan = _last_plan()
-    assert plan.endswith(" + replay_fast<bf16,%d%s>" % (tile, "" if d == tile else ",partial")), plan
+    # a launch this small replays as items of the attention launch (causal, tile dims 32 and 64)
+    assert plan == "attn_fast4<bf16,%d%s> with replay items" % (tile, "" if d == tile else ",partial"), plan
     ref_out, ref_imp = chunked(q, k, v, scale=scale, recency_decay=decay, block=512, dtype=torch.float64)
     assert (out.double() - ref_out.to(out.device)).abs().max().item() <= 2e-2
     assert_importance_close(imp, ref_imp, rtol=1e-3, floor=1e-30)

@@ -136,7 +136,7 @@ def _last_plan():
 @pytest.mark.parametrize("d", [64, 32])
 def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     """Tile dims 32 and 64 run the 4-wave small-grid attention kernel when the 8-wave kernel's
-    items would fill at most two rounds of its resident workgroups. Both compute every row tile
+    items would fill at most one round of its resident workgroups. Both compute every row tile
     the same way (one row tile per wave, 64-key tiles), so batch 0 of a launch big enough for
     the 8-wave kernel equals the small launch of the same data bitwise; the importance differs
     only by FP32 atomic order. fe_last_plan names the kernels each launch ran."""
@@ -149,9 +149,10 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
     small_plan = _last_plan()
     o_big, i_big = _run(q, k, v, True, True, 0.0, 0, use_ws=True)
     big_plan = _last_plan()
-    # every row replayed: in the launch whose attention items fill every resident workgroup, the
-    # heaviest row groups' replay runs as items of the attention launch
-    assert small_plan == "attn_fast4<bf16,%d> + replay_fast<bf16,%d>" % (d, d), small_plan
+    # every row replayed: the small launch replays as items of the attention launch (ascending
+    # row groups); in the launch whose attention items fill every resident workgroup, the heaviest
+    # row groups' replay runs as items, the others on the replay kernel
+    assert small_plan == "attn_fast4<bf16,%d> with replay items" % d, small_plan
     assert big_plan == "attn_fast<bf16,%d> with replay items + replay_fast<bf16,%d>" % (d, d), big_plan
     assert torch.equal(o_small, o_big[:1])
     scale = i_big[:1].abs().amax(dim=-1, keepdim=True)
