@@ -709,6 +709,9 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_SMALL_LAUNCH_ITEMS
 #define FE_SMALL_LAUNCH_ITEMS 1
 #endif
+#ifndef FE_SMALL_LAUNCH_MAX_D
+#define FE_SMALL_LAUNCH_MAX_D 128
+#endif
 #ifndef FE_REPLAY_ITEM_MIN_TILES
 #define FE_REPLAY_ITEM_MIN_TILES 8
 #endif
@@ -941,13 +944,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // eight key tiles where the keys allow (a window of 128 rows at N = 32K otherwise made items of
   // two tiles, 0.4% slower overall).
   bool replay_items = false;
-  // Causal launches at tile dims 32 and 64 whose attention items do not fill the resident
+  // Causal launches at tile dims up to 128 whose attention items do not fill the resident
   // workgroups: a grid of every resident workgroup, and all the replay as items in ascending row
   // groups, so the light rows' replay (their attention items end first) runs beside the heaviest
   // attention items on CUs that would idle, and the replay kernel's launch after the heaviest
-  // item goes (the reference harness's shape at 8K: 8% faster). Without the causal mask every
-  // attention item ends at once (B2 Hq8/Hkv2 N4000 D128 non-causal: 13% slower).
-  if (FE_REPLAY_ITEMS && FE_SMALL_LAUNCH_ITEMS && split && ctr && fast && causal && D <= 64 && plan.rows <= 8 &&
+  // item goes (the reference harness's shape at 8K: 8% faster; B1 Hq8/Hkv2 N4000 D128: 8.6%).
+  // Without the causal mask every attention item ends at once (the same shape non-causal, B2:
+  // 13% slower).
+  if (FE_REPLAY_ITEMS && FE_SMALL_LAUNCH_ITEMS && split && ctr && fast && causal && D <= FE_SMALL_LAUNCH_MAX_D && plan.rows <= 8 &&
       items < resident && items <= kMaxDoneItems) {
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);

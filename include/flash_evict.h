@@ -98,7 +98,7 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  *     output bitwise equal, importance equal up to FP32 atomic order); each waits for its rows' attention item, and runs that item
  *     itself if the wait runs out (a GPU another kernel shares). With longer windows the
  *     heaviest 3% of the row groups replay that way, in the attention launch's tail, and the
- *     second kernel replays the other rows; causal launches at head dims up to 64 too small to
+ *     second kernel replays the other rows; causal launches at head dims up to 128 too small to
  *     fill the GPU replay every row as items, lightest rows first;
  *   * score == 0 uses the counters alone;
  *   * a zero scale runs on the fast kernels with Q zeroed at load (every logit exactly 0).

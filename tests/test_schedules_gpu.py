@@ -176,7 +176,8 @@ def test_small_grid_kernel_at_tile_dims_96_and_128(d, dtype):
     tile = (d + 31) // 32 * 32
     e = "bf16" if dtype == torch.bfloat16 else "f16"
     part = "" if d == tile else ",partial"
-    assert plan == "attn_fast4<%s,%d%s> + replay_fast<%s,%d%s>" % (e, tile, part, e, tile, part), plan
+    # a causal launch this small replays as items of the attention launch
+    assert plan == "attn_fast4<%s,%d%s> with replay items" % (e, tile, part), plan
     o_fu, i_fu = _run(q, k, v, True, True, 0.0, 0, use_ws=False)
     assert torch.equal(o_ws, o_fu)
     assert float((i_ws - i_fu).abs().max()) <= 3e-6 * float(i_fu.abs().max())
