@@ -691,7 +691,7 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #define FE_SMALL_GRID_ROUNDS 1
 #endif
 #ifndef FE_SMALL_GRID_ROUNDS_RT2
-#define FE_SMALL_GRID_ROUNDS_RT2 1.0
+#define FE_SMALL_GRID_ROUNDS_RT2 1.5
 #endif
 
 // Replay items in the two-row-tile attention launch (prefill_impl) for observation windows of at
@@ -891,9 +891,10 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // Small grids at tile dims 32 and 64: where the 8-wave attention kernel's work items would
   // fill at most FE_SMALL_GRID_ROUNDS rounds of its resident workgroups, the 4-wave kernel
   // (twice the items, four workgroups per CU) fills the chip better.
-  // At tile dims 96 and 128, where the two-row-tile kernel's 16-row-tile items would not fill
-  // FE_SMALL_GRID_ROUNDS_RT2 rounds of its workgroups (one per CU), the 4-wave kernel (four row
-  // tiles per item, two workgroups per CU) does.
+  // At tile dims 96 and 128, where the two-row-tile kernel's 16-row-tile items would fill at most
+  // FE_SMALL_GRID_ROUNDS_RT2 (1.5) rounds of its workgroups (one per CU), the 4-wave kernel (four
+  // row tiles per item, two workgroups per CU): 3-12.5% faster at 1.2-1.5 rounds, 2-8% slower at
+  // 1.7-1.8 rounds, 12% slower at 2 (llama8k).
   FusedPlan small;
   if (fast && (plan.rows == 8 || plan.rows == 16) && fast_plan_small(a, dtype, small)) {
     int64_t res = 0;

@@ -1716,8 +1716,9 @@ FusedPlan g_fast[] = {FE_FAST_ENTRIES(F16, "f16"), FE_FAST_ENTRIES(BF16, "bf16")
 // kernel and each SIMD's four waves from four workgroups. Chosen by the launch when the 8-wave
 // kernel's items would fill at most one round of its resident workgroups: the reference
 // harness's Hq4/Hkv2 shape at 8K and 32K (a quarter and one round) measured 11% and 4.4% faster;
-// at two rounds (B1 Hq32/Hkv8 N8192) 4-7% slower, at eight (N32768) 3% slower. At tile dims 96 and 128 (two workgroups per CU) it stands in
-// for attn_rt2_kernel below one round of the latter's items (B2 Hq8/Hkv2 N4000: 30% faster).
+// at two rounds (B1 Hq32/Hkv8 N8192) 4-7% slower, at eight (N32768) 3% slower. At tile dims 96
+// and 128 (two workgroups per CU) it stands in for attn_rt2_kernel up to 1.5 rounds of the latter's
+// items (B2 Hq8/Hkv2 N4000: 30% faster).
 #define FE_FAST_SMALL_DIM(E, e, DP) \
   fast_entry<E, DP, 4, false, false>("attn_fast4<" e "," #DP ">"), fast_entry<E, DP, 4, false, true>("attn_fast4<" e "," #DP ",partial>")
 // [dtype][tile dim 32, 64, 96, 128][partial]

@@ -105,8 +105,8 @@ int64_t fe_replay_rows(int64_t N, int64_t window, float recency_decay);
  * At head dims 72..128 (multiples of 8) the split schedule's attention kernel holds two row
  * tiles per wave and takes a row's reference max over its first 32 keys instead of 64: the
  * output then agrees with fe_prefill's to within two roundings of the probabilities, the
- * importance to FP32 summation order; at other head dims, and for launches too small to fill
- * one round of that kernel's work items (which run one row tile per wave instead), the output
+ * importance to FP32 summation order; at other head dims, and for launches of at most 1.5
+ * rounds of that kernel's work items (which run one row tile per wave instead), the output
  * is bitwise equal and the importance equal up to FP32 atomic order. With room for the biases but not the counters
  * the schedule is static; with less workspace (or NULL) this is fe_prefill. Same reference
  * interface as fe_prefill.

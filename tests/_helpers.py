@@ -70,7 +70,7 @@ def assert_importance_close(imp, ref, rtol=1e-3, floor=1e-30):
 def split_runs_two_row_tiles(d):
     """Whether the split schedule (fe_prefill_ws) may run the two-row-tile attention kernel at
     head dim d in the default build: tile dims 96 and 128 (d a multiple of 8 in 72..128), for
-    launches of at least one round of its work items (smaller ones run the one-row-tile
+    launches of more than 1.5 rounds of its work items (smaller ones run the one-row-tile
     small-grid kernel). Where it does, its reference max comes from a row's first 32 keys, the
     fused kernel's from 64, so callers compare the schedules within a bound instead of bitwise."""
     return d % 8 == 0 and 72 <= d <= 128

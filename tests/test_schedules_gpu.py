@@ -162,7 +162,7 @@ def test_small_grid_kernel_matches_the_eight_wave_kernel(d):
 @pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (120, torch.float16), (96, torch.bfloat16)])
 def test_small_grid_kernel_at_tile_dims_96_and_128(d, dtype):
     """Tile dims 96 and 128 run the 4-wave small-grid attention kernel instead of the two-row-tile
-    kernel when the latter's 16-row-tile items would not fill one round of its workgroups (one
+    kernel when the latter's 16-row-tile items would fill at most 1.5 rounds of its workgroups (one
     per CU). It computes every row tile as the fused single kernel does (one row tile per wave,
     reference max over the first 64 keys): output bitwise equal to fe_prefill's, importance up to
     FP32 atomic order."""
@@ -184,14 +184,14 @@ def test_small_grid_kernel_at_tile_dims_96_and_128(d, dtype):
 
 
 @pytest.mark.parametrize("b,hq,hk,n,d,dtype,causal,decay,window", [
-    # (launches of more than one round of the two-row-tile kernel's items, below which the
+    # (launches of more than 1.5 rounds of the two-row-tile kernel's items, below which the
     # small-grid kernel runs instead)
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.1, 0),       # llama8k's schedule: 1050 rows replayed
-    (2, 8, 2, 9000, 120, torch.float16, True, 0.0, 200),      # partial tile dim, ragged N, fp16
-    (1, 16, 2, 8320, 96, torch.bfloat16, False, 0.0, 100),    # tile dim 96, non-causal
+    (2, 8, 2, 13000, 120, torch.float16, True, 0.0, 200),     # partial tile dim, ragged N, fp16
+    (1, 16, 2, 12400, 96, torch.bfloat16, False, 0.0, 100),   # tile dim 96, non-causal
     # every row replayed: the heaviest row groups as items, the replay kernel for the others
     (1, 32, 8, 8192, 128, torch.bfloat16, True, 0.0, 0),
-    (3, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
+    (4, 12, 4, 5000, 104, torch.float16, True, 0.0, 0),
     # the one-row-tile kernel (fused_fast_kernel) at tile dims 32 and 64: 8 waves, the 4-wave
     # small grid (launches whose attention items fill every resident workgroup)
     (1, 32, 8, 8192, 64, torch.bfloat16, True, 0.1, 0),
