@@ -688,7 +688,7 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 // stands in: for the 8-wave kernel at tile dims 32 and 64, and for the two-row-tile kernel at 96
 // and 128. Build options, for measurement.
 #ifndef FE_SMALL_GRID_ROUNDS
-#define FE_SMALL_GRID_ROUNDS 1
+#define FE_SMALL_GRID_ROUNDS 1.0
 #endif
 #ifndef FE_SMALL_GRID_ROUNDS_RT2
 #define FE_SMALL_GRID_ROUNDS_RT2 1.5
