@@ -935,15 +935,14 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     });
     grid = a.nstatic;
   }
-  // Short observation windows on the two-row-tile attention kernel: the replay runs as work
-  // items of the attention launch, numbered after its attention items (so in every XCD queue
-  // they follow them), each waiting for its rows' attention item to publish their biases (a bit
-  // per attention item after the counters). They fill the end of the attention launch, where
-  // the replay kernel would start only once the last attention item is done. Item = (batch and
-  // KV head, row group of 16 row tiles holding window rows, key range): key ranges chosen for
-  // about two items per resident workgroup (four measured 1.3% slower at llama8k), of at least
-  // eight key tiles where the keys allow (a window of 128 rows at N = 32K otherwise made items of
-  // two tiles, 0.4% slower overall).
+  // Replay items: the replay runs as work items of the attention launch, numbered after its
+  // attention items (so in every XCD queue they follow them), each waiting for its rows' attention
+  // item to publish their biases (a bit per attention item after the counters), or running that
+  // item itself if the wait runs out. Item = (batch and KV head, row group of the attention
+  // kernel's row tiles holding window rows, key range): key ranges chosen for about two items per
+  // resident workgroup (four measured 1.3% slower at llama8k), of at least
+  // FE_REPLAY_ITEM_MIN_TILES key tiles where the keys allow (a window of 128 rows at N = 32K
+  // otherwise made items of two tiles, 0.4% slower overall).
   bool replay_items = false;
   // Causal launches at tile dims up to 128 whose attention items do not fill the resident
   // workgroups: a grid of every resident workgroup, and all the replay as items in ascending row
@@ -952,8 +951,8 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // item goes (the reference harness's shape at 8K: 8% faster; B1 Hq8/Hkv2 N4000 D128: 8.6%).
   // Without the causal mask every attention item ends at once (the same shape non-causal, B2:
   // 13% slower).
-  if (FE_REPLAY_ITEMS && FE_SMALL_LAUNCH_ITEMS && split && ctr && fast && causal && D <= FE_SMALL_LAUNCH_MAX_D && plan.rows <= 8 &&
-      items < resident && items <= kMaxDoneItems) {
+  if (FE_REPLAY_ITEMS && FE_SMALL_LAUNCH_ITEMS && split && ctr && fast && causal && D <= FE_SMALL_LAUNCH_MAX_D &&
+      plan.rows <= 8 && items < resident && items <= kMaxDoneItems) {
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t nwg = B * Hkv * ((int64_t)a.wg_bh - wg_lo);
     const int64_t max_tiles = (N + 63) / 64;
@@ -980,6 +979,9 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // chip (the reference harness's shape at 8K: 5.8% slower).
   const bool item_plan = fast && (plan.rows == 16 || (FE_REPLAY_ITEMS_FAST && plan.rows <= 8 && D <= 64)) &&
                          items >= resident;
+  // Short observation windows (at most FE_REPLAY_ITEMS_MAX of the rows replayed): all the replay
+  // as items, heaviest rows first. They fill the end of the attention launch, where the replay
+  // kernel would start only once the last attention item is done.
   if (FE_REPLAY_ITEMS && !replay_items && split && ctr && item_plan && items <= kMaxDoneItems &&
       (double)(N - a.win_lo) <= FE_REPLAY_ITEMS_MAX * (double)N) {
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
