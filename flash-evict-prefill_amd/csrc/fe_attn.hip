@@ -712,6 +712,11 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_SMALL_LAUNCH_MAX_D
 #define FE_SMALL_LAUNCH_MAX_D 128
 #endif
+// Tail replay items on fused_fast_kernel too (build option: the reference harness's shape at
+// 32K 3% faster with them; D = 64 at the headline head counts within run-to-run drift).
+#ifndef FE_TAIL_FAST
+#define FE_TAIL_FAST 1
+#endif
 #ifndef FE_REPLAY_ITEM_MIN_TILES
 #define FE_REPLAY_ITEM_MIN_TILES 8
 #endif
@@ -1004,7 +1009,7 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
   // replays the rows below them (every row replayed: 0.2-1.4% faster pairs; 6% was slower).
   int64_t tail_groups = 0;
   if (FE_TAIL_REPLAY_FRAC > 0.0 && !replay_items && FE_REPLAY_ITEMS && split && ctr && item_plan &&
-      items <= kMaxDoneItems) {
+      (FE_TAIL_FAST || plan.rows == 16) && items <= kMaxDoneItems) {
     const int64_t wg_lo = ((int64_t)(a.win_lo / 32) * G) / plan.rows;
     const int64_t ng_max = (int64_t)a.wg_bh - wg_lo - 1;
     int64_t ng = (int64_t)ceil(FE_TAIL_REPLAY_FRAC * (double)((int64_t)a.wg_bh - wg_lo));
