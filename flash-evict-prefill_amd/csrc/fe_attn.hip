@@ -717,6 +717,11 @@ int64_t one_shot_grid(int64_t items) { return items + ((items / 8 + 7) & ~(int64
 #ifndef FE_TAIL_FAST
 #define FE_TAIL_FAST 1
 #endif
+// Replay kernel key split in whole rounds of resident blocks for launches without the causal mask
+// (build option).
+#ifndef FE_REPLAY_ROUNDS_SPLIT
+#define FE_REPLAY_ROUNDS_SPLIT 1
+#endif
 #ifndef FE_REPLAY_ITEM_MIN_TILES
 #define FE_REPLAY_ITEM_MIN_TILES 8
 #endif
@@ -1105,14 +1110,30 @@ static int prefill_impl(const void* q, const void* k, const void* v, void* out, 
     const int64_t max_tiles = (N + 63) / 64;
     int64_t rs = (1024 + nwg - 1) / nwg;
     rs = rs < 1 ? 1 : (rs > max_tiles ? max_tiles : rs);
+    int64_t rresident = 0;
+    if ((err = resident_blocks(rplan.fn, 64 * rplan.waves, 0, stream, &rresident)) != hipSuccess) {
+      set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
+      return FE_ERR_HIP;
+    }
+    if (FE_REPLAY_ROUNDS_SPLIT && !causal && nwg > 0 && rresident > 0) {
+      // Without the causal mask every block of a split holds the same key tiles, so the launch
+      // takes whole rounds of resident blocks: choose the split with the fewest key tiles per
+      // resident slot, rounds x (tiles per block + one tile of per-block set-up), the smaller split
+      // on a tie (B2 Hkv2 N4000: 252 row groups x 3 = 756 blocks in one round of 21 key tiles,
+      // instead of x 5 = 1260 blocks in two rounds of 13).
+      int64_t best = -1;
+      for (int64_t s = 1; s <= max_tiles && (s - 1) * nwg <= 4 * rresident; ++s) {
+        const int64_t rounds = (nwg * s + rresident - 1) / rresident;
+        const int64_t cost = rounds * ((max_tiles + s - 1) / s + 1);
+        if (best < 0 || cost < best) {
+          best = cost;
+          rs = s;
+        }
+      }
+    }
     r.rsplit = (int)rs;
     int64_t rgrid = nwg * rs;
     if (ctr) {
-      int64_t rresident = 0;
-      if ((err = resident_blocks(rplan.fn, 64 * rplan.waves, 0, stream, &rresident)) != hipSuccess) {
-        set_error(std::string("fe_prefill: occupancy query: ") + hipGetErrorString(err));
-        return FE_ERR_HIP;
-      }
       r.queue = ctr + kQueueReplay;
       r.nitems = (int)rgrid;
       r.nstatic = (int)(rgrid < rresident ? rgrid : rresident);
