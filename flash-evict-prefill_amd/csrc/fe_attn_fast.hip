@@ -459,10 +459,11 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
     // sum would leave that key's rounding error, up to 2^-8 relative in bf16, in the output).
     // The replay bias needs the FP32 sum of the unrounded probabilities (l_run, replay rows
     // only): b = m + log2 l_run does not depend on the choice of m. A tile some lane of which
-    // sums to more than E::kMaxTileSum (inf included) takes a new exact max, rescales O and
-    // both sums and recomputes its probabilities, which are then at most 1. For random inputs
-    // that happens on a few percent of tiles, where following the exact running max rescaled
-    // O on ~40% of them, and no tile spends instructions on a row max.
+    // sums to more than E::kMaxTileSum (inf included) takes a new reference (its exact max plus
+    // E::kRescaleHeadroom), rescales O and both sums and recomputes its probabilities, which are
+    // then at most 1. For random inputs that happens on a few percent of tiles, where following
+    // the exact running max rescaled O on ~40% of them, and no tile spends instructions on a row
+    // max.
     auto exact_max = [&](const f32x16(&sacc)[2]) __attribute__((always_inline)) -> float {
       // max over the 32 keys of this lane and the other half-wave: two chains of three-input
       // maxima (v_maximum3_f32, two new values each), 16 instructions for 32 values
@@ -556,11 +557,11 @@ __global__ __launch_bounds__(NW * 64, (FastOccupancy<NW, DP>::WAVES_PER_EU)) voi
       // exponentials), else the rounded one
       const float guard = decltype(exact_tag)::value ? le : (pr[0] + pr[1]) + (pr[2] + pr[3]);
       if (__any(guard > E::kMaxTileSum)) {
-        // S again (the tile is still in LDS), the new exact max, O and both sums rescaled,
-        // probabilities recomputed: now all at most 1
+        // S again (the tile is still in LDS), the new reference (the exact max plus the type's
+        // headroom), O and both sums rescaled, probabilities recomputed: now all at most 1
         qk_tile(kb, BUF, SLOT, sacc);
         const float mt = exact_max(sacc);
-        const float mn = vmax(m_run, mt);
+        const float mn = vmax(m_run, mt + E::kRescaleHeadroom);
         const float corr = mn > m_run ? fast_exp2(m_run - mn) : 1.f;
         l_run *= corr;
         l_rnd *= corr;
@@ -1178,8 +1179,8 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       else
         return 0.f;
     };
-    // overflow path of row tile J: S again, the new exact max, O and both sums rescaled,
-    // probabilities recomputed (now at most 1)
+    // overflow path of row tile J: S again, the new reference (the exact max plus the type's
+    // headroom), O and both sums rescaled, probabilities recomputed (now at most 1)
     auto rescale_one = [&](auto exact_tag, auto jtag, int kh, int BUF, int SLOT, int s, u32x4(&pb)[2], float(&pr)[4])
                            __attribute__((always_inline)) -> float {
       constexpr int J = decltype(jtag)::value;
@@ -1187,7 +1188,7 @@ __global__ __launch_bounds__(512, 2) void attn_rt2_kernel(const AttnArgs a) {
       qk_one(jtag, kh, BUF, SLOT, s, S);
       // a row that overflows has a finite reference max (its tile is a real one)
       const float m_old = -nm[J];
-      const float mn = vmax(m_old, exact_max(S));
+      const float mn = vmax(m_old, exact_max(S) + E::kRescaleHeadroom);
       const float corr = mn > m_old ? fast_exp2(m_old - mn) : 1.f;
       l_run[J] *= corr;
       l_rnd[J] *= corr;

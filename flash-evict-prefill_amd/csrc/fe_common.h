@@ -17,6 +17,11 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // Element tags: storage is always 16-bit; the tag selects MFMA flavour and rounding.
+// Rescale headroom of the bf16 attention kernels (build option; 0 takes the exact max).
+#ifndef FE_RESCALE_HEADROOM_BF16
+#define FE_RESCALE_HEADROOM_BF16 16.f
+#endif
+
 struct BF16 {
   typedef __bf16 scalar;
   // Largest per-lane sum of one step's probabilities (relative to a row's reference max)
@@ -29,6 +34,11 @@ struct BF16 {
   // not there; below 2^95 / ceil(N/32) every rounding is relative, and scaling V by a power
   // of two scales the output and importance exactly.
   static constexpr float kMaxTileSum = 4294967296.f;
+  // A step that overflows takes as its new reference the step's exact max plus this headroom
+  // (log2 units), so that later keys may rise 32 + 16 above the step's max before the next
+  // rescale. Its probabilities are then at most 2^-16, which bf16 and FP32 hold with full
+  // relative precision; rows that never overflow are unaffected.
+  static constexpr float kRescaleHeadroom = FE_RESCALE_HEADROOM_BF16;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -62,6 +72,9 @@ struct F16 {
   typedef _Float16 scalar;
   // probabilities stay below the fp16 maximum; |O| < 2^16 * ceil(N/32) * 65504 is always finite
   static constexpr float kMaxTileSum = 32768.f;
+  // no headroom: probabilities far below the reference max would fall into fp16's subnormal
+  // range, where the rounding of P for P@V is no longer relative
+  static constexpr float kRescaleHeadroom = 0.f;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
